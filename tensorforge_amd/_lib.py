@@ -1,0 +1,188 @@
+"""ctypes bindings of libtforge_hip.so (declared in include/tforge_hip.h).
+
+The library must have been built (python -m tensorforge_amd.build); there is
+no fallback: every call on the hot path goes through the gfx950 kernels.
+"""
+
+import ctypes
+import pathlib
+
+PKG = pathlib.Path(__file__).resolve().parent
+LIB_PATH = PKG / "libtforge_hip.so"
+
+TF_MODE_KERNEL, TF_MODE_BLAS = 0, 1
+FAMILY_NAMES = {0: "direct", 1: "staged", 2: "elementwise"}
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 256), ("arch", ctypes.c_char * 64), ("compute_units", ctypes.c_int),
+                ("max_clock_mhz", ctypes.c_int), ("lds_bytes_per_cu", ctypes.c_int),
+                ("max_threads_per_cu", ctypes.c_int), ("l2_bytes", ctypes.c_longlong),
+                ("global_mem_bytes", ctypes.c_longlong), ("driver_version", ctypes.c_int),
+                ("runtime_version", ctypes.c_int)]
+
+
+class LaunchInfo(ctypes.Structure):
+    _fields_ = [("kernel", ctypes.c_char * 96), ("args", ctypes.c_char * 160), ("ops", ctypes.c_char * 96),
+                ("family", ctypes.c_int), ("grid", ctypes.c_int * 3), ("block", ctypes.c_int * 3),
+                ("m", ctypes.c_longlong), ("n", ctypes.c_longlong), ("k", ctypes.c_longlong),
+                ("lds_bytes", ctypes.c_int)]
+
+
+class KernelResources(ctypes.Structure):
+    _fields_ = [("regs", ctypes.c_int), ("local_bytes", ctypes.c_int), ("static_smem", ctypes.c_int),
+                ("blocks_per_cu", ctypes.c_int), ("theo_occupancy", ctypes.c_double), ("threads", ctypes.c_int)]
+
+
+class BufferInfo(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 64), ("role", ctypes.c_int), ("rows", ctypes.c_longlong),
+                ("cols", ctypes.c_longlong)]
+
+
+class BenchResult(ctypes.Structure):
+    _fields_ = [("median_ms", ctypes.c_double), ("min_ms", ctypes.c_double), ("mean_ms", ctypes.c_double),
+                ("std_ms", ctypes.c_double), ("clock_median_mhz", ctypes.c_double),
+                ("clock_min_mhz", ctypes.c_double), ("clock_max_mhz", ctypes.c_double),
+                ("power_median_w", ctypes.c_double), ("warmup", ctypes.c_int), ("reps", ctypes.c_int),
+                ("l2_flush", ctypes.c_int), ("padded", ctypes.c_longlong * 3)]
+
+
+# (name, restype, argtypes) of every exported function, in header order.
+P, I, LL, U = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_uint
+SIGNATURES = [
+    ("tf_last_error", ctypes.c_char_p, []),
+    ("tf_device_info", I, [ctypes.POINTER(DeviceInfo)]),
+    ("tf_compile", I, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(P)]),
+    ("tf_kernel_free", None, [P]),
+    ("tf_kernel_num_launches", I, [P]),
+    ("tf_kernel_launch_info", I, [P, I, ctypes.POINTER(LaunchInfo)]),
+    ("tf_kernel_num_buffers", I, [P]),
+    ("tf_kernel_buffer_info", I, [P, I, ctypes.POINTER(BufferInfo)]),
+    ("tf_kernel_info", I, [P, I, ctypes.POINTER(KernelResources)]),
+    ("tf_launch", I, [P, ctypes.POINTER(P), P]),
+    ("tf_run", I, [P, I, ctypes.POINTER(LL), ctypes.POINTER(ctypes.POINTER(ctypes.c_float)),
+                   ctypes.POINTER(ctypes.c_float)]),
+    ("tf_bench", I, [P, I, ctypes.POINTER(LL), ctypes.POINTER(ctypes.POINTER(ctypes.c_float)), U, I, I, I,
+                     ctypes.POINTER(BenchResult)]),
+    ("tf_bench_samples", I, [P, ctypes.POINTER(ctypes.c_double), I]),
+    ("tf_registry_size", I, []),
+    ("tf_registry_entry", I, [I, ctypes.POINTER(I), ctypes.POINTER(I), ctypes.c_char_p, I]),
+]
+
+_lib = None
+
+
+def lib():
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m tensorforge_amd.build` "
+                               "(the gfx950 kernels are the only execution path)")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, res, args in SIGNATURES:
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc < 0:
+        raise RuntimeError(lib().tf_last_error().decode())
+    return rc
+
+
+class Kernel:
+    """A compiled tforge program (owns the tf_kernel_t handle)."""
+
+    def __init__(self, program, options="", source_name="input.mlir"):
+        L = lib()
+        self.h = P()
+        check(L.tf_compile(source_name.encode(), program.encode(), options.encode(), ctypes.byref(self.h)))
+        self.program, self.options = program, options
+
+    def __del__(self):
+        h = getattr(self, "h", None)
+        if h and _lib is not None:
+            _lib.tf_kernel_free(h)
+            self.h = None
+
+    def launches(self):
+        L, out = lib(), []
+        for i in range(check(L.tf_kernel_num_launches(self.h))):
+            li = LaunchInfo()
+            check(L.tf_kernel_launch_info(self.h, i, ctypes.byref(li)))
+            out.append({"kernel": li.kernel.decode(), "grid": list(li.grid), "block": list(li.block),
+                        "args": li.args.decode().split(","), "ops": li.ops.decode(),
+                        "family": FAMILY_NAMES[li.family], "m": li.m, "n": li.n, "k": li.k,
+                        "lds_bytes": li.lds_bytes})
+        return out
+
+    def buffers(self):
+        L, out = lib(), []
+        for i in range(check(L.tf_kernel_num_buffers(self.h))):
+            bi = BufferInfo()
+            check(L.tf_kernel_buffer_info(self.h, i, ctypes.byref(bi)))
+            out.append({"name": bi.name.decode(), "role": "output" if bi.role == 1 else "input",
+                        "shape": (bi.rows, bi.cols)})
+        return out
+
+    def resources(self, launch=0):
+        r = KernelResources()
+        check(lib().tf_kernel_info(self.h, launch, ctypes.byref(r)))
+        return {"regs": r.regs, "local_bytes": r.local_bytes, "static_smem": r.static_smem,
+                "blocks_per_sm": r.blocks_per_cu, "theo_occupancy": round(r.theo_occupancy, 3),
+                "threads": r.threads}
+
+    def launch(self, device_ptrs, stream=0):
+        arr = (P * len(device_ptrs))(*[P(int(p)) for p in device_ptrs])
+        check(lib().tf_launch(self.h, arr, P(int(stream)) if stream else None))
+
+    @staticmethod
+    def _host_ptrs(arrays):
+        arr = (ctypes.POINTER(ctypes.c_float) * len(arrays))()
+        for i, a in enumerate(arrays):
+            arr[i] = a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+        return arr
+
+    @staticmethod
+    def _logical(mnk):
+        return None if mnk is None else (LL * 3)(*[int(x) for x in mnk])
+
+    def run(self, inputs, out, mode=TF_MODE_KERNEL, logical=None):
+        check(lib().tf_run(self.h, mode, self._logical(logical), self._host_ptrs(inputs),
+                           out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+        return out
+
+    def bench(self, inputs=None, mode=TF_MODE_KERNEL, logical=None, seed=1234, warmup=10, reps=100, flush=False):
+        r = BenchResult()
+        ptrs = self._host_ptrs(inputs) if inputs is not None else None
+        check(lib().tf_bench(self.h, mode, self._logical(logical), ptrs, seed, warmup, reps, int(flush),
+                             ctypes.byref(r)))
+        return r
+
+    def samples(self, cap=100000):
+        buf = (ctypes.c_double * cap)()
+        n = check(lib().tf_bench_samples(self.h, buf, cap))
+        return list(buf[:n])
+
+
+def device_info():
+    d = DeviceInfo()
+    check(lib().tf_device_info(ctypes.byref(d)))
+    return {"name": d.name.decode(), "arch": d.arch.decode(), "compute_units": d.compute_units,
+            "max_clock_mhz": d.max_clock_mhz, "lds_bytes_per_cu": d.lds_bytes_per_cu,
+            "max_threads_per_cu": d.max_threads_per_cu, "l2_bytes": d.l2_bytes,
+            "global_mem_bytes": d.global_mem_bytes, "driver_version": d.driver_version,
+            "runtime_version": d.runtime_version}
+
+
+def registry():
+    L, out = lib(), []
+    fam, cfg, name = I(), (I * 7)(), ctypes.create_string_buffer(96)
+    for i in range(L.tf_registry_size()):
+        check(L.tf_registry_entry(i, ctypes.byref(fam), cfg, name, 96))
+        out.append({"family": FAMILY_NAMES[fam.value], "cfg": tuple(cfg), "name": name.value.decode()})
+    return out

@@ -1,0 +1,220 @@
+"""Analytical cost model of the staged GEMM kernel, retargeted to CDNA4 (MI355X).
+
+The reference's Stage 9 model (python/costmodel.py:1-97) predicts the time of
+its SIMT staged kernel from the tile sizes, the padded problem and the blocks
+per SM reported by the occupancy API.  Its skeleton is kept:
+
+  blocks   = (Mp / BM) * (Np / BN)
+  waves    = ceil(blocks / (UNITS * blocks_per_unit))      rounds of resident blocks
+  resident = min(blocks_per_unit, ceil(blocks / UNITS))
+  cycles   = waves * (Kp / BK) * step
+  time     = max(cycles / clock, compulsory_bytes / DRAM_BW)
+
+and `predict(..., target=SM120)` restates the reference formula exactly (the
+test suite checks it against every 4th row of the reference's own
+stage9_autotune.csv and e2_a6000_autotune.csv notes).  The MI355X target
+replaces the per-step terms with what bounds the gfx950 MFMA kernel:
+
+  mfma_step  FP32 MFMA issue on the busiest SIMD: the resident waves share 4
+             SIMDs (q = ceil(resident * W / 4) waves per SIMD), and a wave's
+             slab is FM*FN*(BK/2) v_mfma_f32_32x32x2 of 64 cycles each.
+  lds_step   LDS bytes per slab over 128 B/clk: per wave (BK/8)*1 KiB per
+             32-row A block (b128 reads) and per 32-column B block (b32
+             reads), plus the block's (BM+BN)*BK*4 B of stores.
+  l2_step    global -> LDS bytes per slab, (BM+BN)*BK*4 per block, over the
+             L2 bandwidth share of a CU (64 B/clk).
+  exposed    the next slab's loads are in flight during the current slab
+             (double buffering): max(0, LATENCY - compute) is exposed.
+  sync       one barrier per slab; its bubble is hidden by other waves on the
+             SIMD, so it is divided by q.
+
+Constants are AMD's published MI355X figures (256 CUs, 2.4 GHz, FP32 matrix
+256 FLOP/clk/CU, 160 KiB LDS, 8 TB/s HBM); LATENCY and SYNC are assumptions
+calibrated on measurements, and the model only ranks configurations.
+"""
+
+import dataclasses
+import json
+import math
+import os
+import pathlib
+
+PKG = pathlib.Path(__file__).resolve().parent
+
+
+@dataclasses.dataclass(frozen=True)
+class Target:
+    name: str
+    kind: str               # "simt" (reference formula) or "mfma" (CDNA4)
+    units: int              # SMs or CUs
+    clock_mhz: float
+    dram_bw: float          # bytes/s
+    fma_per_cycle: float = 128.0        # simt: FP32 FMA lanes per SM
+    smem_words_per_cycle: float = 32.0  # simt
+    latency: float = 600.0              # cycles, global load missing L1
+    lds_bytes_per_cycle: float = 128.0  # mfma
+    l2_bytes_per_cycle: float = 64.0    # mfma, per CU
+    sync: float = 160.0                 # mfma, barrier bubble per slab
+    simds: int = 4
+    mfma_cycles: float = 64.0           # v_mfma_f32_32x32x2_f32 per wave
+    lds_per_cu: int = 160 * 1024
+    max_waves_per_simd: int = 8
+
+
+# The reference's model (python/costmodel.py:41-46); TF_GPU_SMS / TF_GPU_DRAM_BW as there.
+SM120 = Target("sm_120", "simt", int(os.environ.get("TF_GPU_SMS", "188")), 2280.0,
+               float(os.environ.get("TF_GPU_DRAM_BW", "1530e9")))
+MI355X = Target("gfx950", "mfma", int(os.environ.get("TF_GPU_CUS", "256")), 2400.0,
+                float(os.environ.get("TF_GPU_HBM_BW", "8e12")), latency=900.0)
+
+SMS = MI355X.units
+CLOCK_MHZ = MI355X.clock_mhz
+
+
+def _valid_staged(bm, bn, tm, tn, bk):
+    if bm % tm or bn % tn:
+        return False
+    threads = (bm // tm) * (bn // tn)
+    if threads % 64 or threads > 1024:
+        return False
+    wtm, wtn = 8 * tm, 8 * tn
+    if wtm % 32 or wtn % 32 or bm % wtm or bn % wtn or bk % 8:
+        return False
+    return 2 * (bm * (bk + 4) + bk * (bn + 8)) * 4 <= 160 * 1024
+
+
+def reference_space():
+    """The reference's Stage 9 grid (python/costmodel.py:49-60)."""
+    out = []
+    for bm in (32, 64, 128):
+        for bn in (32, 64, 128):
+            for tm, tn in ((4, 4), (8, 4), (4, 8), (8, 8)):
+                for bk in (8, 16, 32):
+                    threads = (bm // tm) * (bn // tn)
+                    if bm % tm or bn % tn or not 32 <= threads <= 1024:
+                        continue
+                    out.append((bm, bn, tm, tn, bk))
+    return out
+
+
+def config_space():
+    """The CDNA4 grid: BM, BN in {32..256}, TM x TN in {4x4, 8x4, 4x8, 8x8},
+    BK in {8..64}, every configuration that has a gfx950 instantiation (whole
+    waves of 32x32 MFMA blocks, LDS within 160 KiB)."""
+    out = []
+    for bm in (32, 64, 128, 256):
+        for bn in (32, 64, 128, 256):
+            for tm, tn in ((4, 4), (8, 4), (4, 8), (8, 8)):
+                for bk in (8, 16, 32, 64):
+                    if _valid_staged(bm, bn, tm, tn, bk):
+                        out.append((bm, bn, tm, tn, bk))
+    return out
+
+
+def options(cfg):
+    bm, bn, tm, tn, bk = cfg
+    return f"block-tile={bm},{bn} thread-tile={tm},{tn} tile-k={bk} promote=1 vectorize=1"
+
+
+def name(cfg):
+    bm, bn, tm, tn, bk = cfg
+    return f"b{bm}x{bn}-t{tm}x{tn}-k{bk}"
+
+
+def kernel_name(cfg):
+    bm, bn, tm, tn, bk = cfg
+    return f"tf_staged_b{bm}x{bn}_t{tm}x{tn}_k{bk}"
+
+
+def _resources():
+    p = PKG / "kernel_resources.json"
+    return json.loads(p.read_text()) if p.exists() else {}
+
+
+def estimate_info(cfg, target=MI355X, resources=None):
+    """Blocks per CU without a GPU: the smaller of the register-limited waves
+    per SIMD (compiler resource remarks) and the LDS limit; the occupancy API
+    (tforge_gpu.info) gives the same number on the device."""
+    bm, bn, tm, tn, bk = cfg
+    threads = (bm // tm) * (bn // tn)
+    w = threads // 64
+    rec = (resources if resources is not None else _resources()).get(kernel_name(cfg), {})
+    occ = rec.get("occupancy_waves_per_simd", target.max_waves_per_simd)
+    if occ is None or occ <= 0:
+        occ = target.max_waves_per_simd
+    lds = rec.get("lds_bytes", 2 * (bm * (bk + 4) + bk * (bn + 8)) * 4)
+    by_regs = (occ * target.simds) // w
+    by_lds = target.lds_per_cu // lds if lds else by_regs
+    return {"blocks_per_sm": max(1, min(by_regs, by_lds, 2048 // threads)), "threads": threads}
+
+
+def predict(cfg, padded, info, clock_mhz=None, target=MI355X):
+    """Predicted time in ms and the terms that produced it."""
+    bm, bn, tm, tn, bk = cfg
+    mp, np_, kp = padded
+    clock = clock_mhz or target.clock_mhz
+    bps = max(1, info["blocks_per_sm"])
+    threads = (bm // tm) * (bn // tn)
+    blocks = (mp // bm) * (np_ // bn)
+    waves = math.ceil(blocks / (target.units * bps))
+    resident = min(bps, math.ceil(blocks / target.units))
+    if target.kind == "simt":
+        # python/costmodel.py:74-97, unchanged.
+        fma_step = bm * bn * bk / target.fma_per_cycle
+        lds_step = threads * bk * (tm + tn) / target.smem_words_per_cycle
+        compute_step = max(fma_step, lds_step)
+        exposed = max(0.0, target.latency - (resident - 1) * compute_step)
+        step = resident * compute_step + exposed
+        cycles = waves * (kp // bk) * step
+        t_compute = cycles / (clock * 1e6)
+        t_dram = 4.0 * (mp * kp + kp * np_ + mp * np_) / target.dram_bw
+        t = max(t_compute, t_dram)
+        return {"pred_ms": t * 1e3, "waves": waves, "resident": resident, "blocks": blocks,
+                "fma_step": fma_step, "lds_step": lds_step,
+                "bound": "dram" if t_dram > t_compute else ("smem" if lds_step > fma_step else "fma"),
+                "latency_exposed": exposed > 0, "intensity": 2.0 * bm * bn / (4.0 * (bm + bn))}
+    w = threads // 64
+    fm, fn = tm // 4, tn // 4
+    q = math.ceil(resident * w / target.simds)
+    mfma_step = q * fm * fn * (bk / 2) * target.mfma_cycles
+    lds_bytes = resident * (w * (bk / 8) * 1024 * (fm + fn) + (bm + bn) * bk * 4)
+    lds_step = lds_bytes / target.lds_bytes_per_cycle
+    l2_step = resident * (bm + bn) * bk * 4 / target.l2_bytes_per_cycle
+    compute = max(mfma_step, lds_step, l2_step)
+    exposed = max(0.0, target.latency - compute)
+    step = compute + exposed + target.sync / q
+    epilogue = target.latency + resident * bm * bn * 4 / target.l2_bytes_per_cycle
+    cycles = waves * ((kp // bk) * step + target.latency + epilogue)
+    t_compute = cycles / (clock * 1e6)
+    t_dram = 4.0 * (mp * kp + kp * np_ + mp * np_ + np_) / target.dram_bw
+    t = max(t_compute, t_dram)
+    terms = {"mfma": mfma_step, "lds": lds_step, "l2": l2_step}
+    bound = "dram" if t_dram > t_compute else max(terms, key=terms.get)
+    return {"pred_ms": t * 1e3, "waves": waves, "resident": resident, "blocks": blocks,
+            "fma_step": mfma_step, "lds_step": lds_step, "l2_step": l2_step, "bound": bound,
+            "latency_exposed": exposed > 0, "waves_per_simd": q,
+            "intensity": 2.0 * bm * bn / (4.0 * (bm + bn))}
+
+
+def padded(cfg, m, n, k):
+    bm, bn, _, _, bk = cfg
+    up = lambda x, t: -(-x // t) * t
+    return up(m, bm), up(n, bn), up(k, bk)
+
+
+def rank(m, n, k, space=None, target=MI355X, infos=None):
+    """Configurations sorted by predicted time (model pick first)."""
+    res = _resources()
+    space = space or config_space()
+    scored = []
+    for cfg in space:
+        inf = (infos or {}).get(cfg) or estimate_info(cfg, target, res)
+        scored.append((predict(cfg, padded(cfg, m, n, k), inf, target=target)["pred_ms"], cfg))
+    scored.sort()
+    return [c for _, c in scored]
+
+
+def default_config(m, n, k):
+    """The cost model's pick for a shape: what the backend uses when no
+    autotuned configuration is recorded."""
+    return rank(m, n, k)[0]

@@ -1,0 +1,105 @@
+// Direct (no K staging) GEMM family and the element-op kernels.
+//
+// Direct GEMM: what the reference pipeline emits for "tile-k=0" options, its
+// default (docs/stage7.md:9-20; lib/Transforms/Gpu.cpp:188-197): the launch is
+// grid (ceil(N/BN), ceil(M/BM)) x block (BN/TN, BM/TM), each thread owns a
+// TM x TN sub-tile of its block tile and runs the K loop from +0.0 with one
+// fused multiply-add per k, in sequential k order, then the fused epilogue.
+// That arithmetic is bit-identical to the reference's naive kernel
+// (docs/numerics.md:53), any shape is accepted and edges are masked.
+//
+// Element-op kernels: programs with no matmul (tforge.bias_add / relu / add
+// alone, or chains of them) run one thread per TM x TN elements with the same
+// launch geometry, one IEEE operation per op, so results are bit-exact against
+// NumPy float32 (python/tforge_gpu.py:116-126).
+#include "epilogue.hpp"
+
+namespace tfk {
+
+template <int TM, int TN>
+__global__ void direct_gemm_kernel(GemmParams p) {
+  const long m_base = ((long)blockIdx.y * blockDim.y + threadIdx.y) * TM;
+  const long n_base = ((long)blockIdx.x * blockDim.x + threadIdx.x) * TN;
+  if (m_base >= p.M || n_base >= p.N) return;
+  float acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = 0.0f;
+  const bool full = m_base + TM <= p.M && n_base + TN <= p.N;
+  for (int k = 0; k < p.K; ++k) {
+    float a[TM], b[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a[i] = (full || m_base + i < p.M) ? p.A[(m_base + i) * p.lda + k] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) b[j] = (full || n_base + j < p.N) ? p.B[(long)k * p.ldb + n_base + j] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const long m = m_base + i, n = n_base + j;
+      if (m < p.M && n < p.N) p.C[m * p.ldc + n] = apply_epi1(acc[i][j], p.epi, m, (int)n);
+    }
+}
+
+template <int TM, int TN>
+__global__ void elementwise_kernel(EltParams p) {
+  const long m_base = ((long)blockIdx.y * blockDim.y + threadIdx.y) * TM;
+  const long n_base = ((long)blockIdx.x * blockDim.x + threadIdx.x) * TN;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const long m = m_base + i, n = n_base + j;
+      if (m < p.M && n < p.N) p.Y[m * p.ldy + n] = apply_epi1(p.X[m * p.ldx + n], p.epi, m, (int)n);
+    }
+}
+
+template <int TM, int TN>
+hipError_t launch_direct(const GemmParams &p, dim3 grid, dim3 block, hipStream_t stream) {
+  hipLaunchKernelGGL((direct_gemm_kernel<TM, TN>), grid, block, 0, stream, p);
+  return hipGetLastError();
+}
+
+template <int TM, int TN>
+hipError_t launch_elementwise(const EltParams &p, dim3 grid, dim3 block, hipStream_t stream) {
+  hipLaunchKernelGGL((elementwise_kernel<TM, TN>), grid, block, 0, stream, p);
+  return hipGetLastError();
+}
+
+// The registry tables are host data (they hold host launch stubs).
+#ifndef __HIP_DEVICE_COMPILE__
+#define TF_DIRECT(TM, TN)                                                                       \
+  KernelEntry{FAM_DIRECT, 0, 0, TM, TN, 0, 0, 0, "tf_direct_t" #TM "x" #TN,                   \
+              reinterpret_cast<const void *>(&direct_gemm_kernel<TM, TN>), &launch_direct<TM, TN>, \
+              nullptr, 0}
+#define TF_ELT(TM, TN)                                                                          \
+  KernelEntry{FAM_ELEMENTWISE, 0, 0, TM, TN, 0, 0, 0, "tf_elementwise_t" #TM "x" #TN,         \
+              reinterpret_cast<const void *>(&elementwise_kernel<TM, TN>), nullptr,             \
+              &launch_elementwise<TM, TN>, 0}
+#define TF_BOTH(TM, TN) TF_DIRECT(TM, TN), TF_ELT(TM, TN)
+
+// Thread tiles 1, 2, 4, 8 in each dimension.
+extern const KernelEntry kDirectEntries[] = {
+    TF_BOTH(1, 1), TF_BOTH(1, 2), TF_BOTH(1, 4), TF_BOTH(1, 8), TF_BOTH(2, 1), TF_BOTH(2, 2),
+    TF_BOTH(2, 4), TF_BOTH(2, 8), TF_BOTH(4, 1), TF_BOTH(4, 2), TF_BOTH(4, 4), TF_BOTH(4, 8),
+    TF_BOTH(8, 1), TF_BOTH(8, 2), TF_BOTH(8, 4), TF_BOTH(8, 8),
+};
+extern const int kDirectCount = sizeof(kDirectEntries) / sizeof(kDirectEntries[0]);
+#else
+// Device pass: instantiate the kernels the host table names.
+#define TF_INST(TM, TN)                                                  \
+  template __global__ void direct_gemm_kernel<TM, TN>(GemmParams);       \
+  template __global__ void elementwise_kernel<TM, TN>(EltParams);
+TF_INST(1, 1) TF_INST(1, 2) TF_INST(1, 4) TF_INST(1, 8)
+TF_INST(2, 1) TF_INST(2, 2) TF_INST(2, 4) TF_INST(2, 8)
+TF_INST(4, 1) TF_INST(4, 2) TF_INST(4, 4) TF_INST(4, 8)
+TF_INST(8, 1) TF_INST(8, 2) TF_INST(8, 4) TF_INST(8, 8)
+#endif  // __HIP_DEVICE_COMPILE__
+
+}  // namespace tfk

@@ -1,0 +1,51 @@
+// Device-side epilogue: the fused tforge element ops applied to accumulators.
+#pragma once
+
+#include "tf_kernels.h"
+
+namespace tfk {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// IEEE-754-2019 maximum(x, +0.0), the semantics of tforge.relu
+// (docs/dialect.md:26-30): NaN propagates and -0.0 maps to +0.0.  v_max_f32
+// would return +0.0 for a NaN input, so the select is written out.
+__device__ __forceinline__ float relu_ieee(float x) { return (x > 0.0f || x != x) ? x : 0.0f; }
+
+// Applies the epilogue to four consecutive outputs C[m, n..n+3].
+__device__ __forceinline__ f32x4 apply_epi4(f32x4 v, const EpiParams &e, long m, int n) {
+#pragma unroll
+  for (int i = 0; i < kMaxEpi; ++i) {
+    if (i >= e.nops) break;
+    const int kind = e.kind[i];
+    if (kind == EPI_BIAS) {
+      v += *reinterpret_cast<const f32x4 *>(e.ptr[i] + n);
+    } else if (kind == EPI_RELU) {
+      v.x = relu_ieee(v.x);
+      v.y = relu_ieee(v.y);
+      v.z = relu_ieee(v.z);
+      v.w = relu_ieee(v.w);
+    } else if (kind == EPI_ADD) {
+      v += *reinterpret_cast<const f32x4 *>(e.ptr[i] + m * e.ldr[i] + n);
+    } else if (kind == EPI_ADD_SELF) {
+      v = v + v;
+    }
+  }
+  return v;
+}
+
+// Scalar form for edge elements and the direct / elementwise kernels.
+__device__ __forceinline__ float apply_epi1(float v, const EpiParams &e, long m, int n) {
+#pragma unroll
+  for (int i = 0; i < kMaxEpi; ++i) {
+    if (i >= e.nops) break;
+    const int kind = e.kind[i];
+    if (kind == EPI_BIAS) v = v + e.ptr[i][n];
+    else if (kind == EPI_RELU) v = relu_ieee(v);
+    else if (kind == EPI_ADD) v = v + e.ptr[i][m * e.ldr[i] + n];
+    else if (kind == EPI_ADD_SELF) v = v + v;
+  }
+  return v;
+}
+
+}  // namespace tfk

@@ -1,0 +1,109 @@
+"""Generate the ahead-of-time instantiation list of the staged gfx950 GEMM kernel.
+
+Every staged configuration a pipeline option string can select must exist as a
+template instantiation in libtforge_hip.so.  This script writes
+_gen/staged_XX.hip (one shard per parallel compile job) and _gen/registry.hip,
+which tf_compile searches at run time.
+
+The configuration space is the reference's Stage 9 grid (python/costmodel.py:49-60:
+BM, BN in {32, 64, 128}, TM x TN in {4x4, 8x4, 4x8, 8x8}, BK in {8, 16, 32}),
+widened for CDNA4 (BM, BN up to 256, BK up to 64), restricted to the
+configurations that map onto whole waves of 32x32 MFMA blocks, plus the
+promote/vectorize ablation variants of the reference's Stage 8/9 ladders
+(bench/stage8_gpu.sh:7-14, bench/stage9_ablation.py:23-28).
+"""
+
+import pathlib
+import sys
+
+HERE = pathlib.Path(__file__).resolve().parent
+LDS_LIMIT = 160 * 1024
+
+
+def staged_valid(bm, bn, tm, tn, bk, promote=1):
+    """Why a staged config cannot be instantiated, or None if it can."""
+    if bm % tm or bn % tn:
+        return "block tile must be a multiple of the thread tile"
+    threads = (bm // tm) * (bn // tn)
+    if threads % 64:
+        return f"{threads} threads per block is not a whole number of 64-lane waves"
+    if threads > 1024:
+        return f"{threads} threads per block exceeds 1024"
+    wtm, wtn = 8 * tm, 8 * tn
+    if wtm % 32 or wtn % 32:
+        return f"wave tile {wtm}x{wtn} (8*TM x 8*TN) is not made of 32x32 MFMA blocks"
+    if bm % wtm or bn % wtn:
+        return f"block tile {bm}x{bn} is not a multiple of the wave tile {wtm}x{wtn} (8*TM x 8*TN)"
+    if bk % 8:
+        return "tile-k must be a multiple of 8"
+    lds = 2 * (bm * (bk + 4) + bk * (bn + 8)) * 4 if promote else 0
+    if lds > LDS_LIMIT:
+        return f"LDS {lds} B exceeds 160 KiB"
+    return None
+
+
+def configs():
+    out = []
+    for bm in (32, 64, 128, 256):
+        for bn in (32, 64, 128, 256):
+            for tm, tn in ((4, 4), (8, 4), (4, 8), (8, 8)):
+                for bk in (8, 16, 32, 64):
+                    if staged_valid(bm, bn, tm, tn, bk) is None:
+                        out.append((bm, bn, tm, tn, bk, 1, 1))
+    for bm, bn, tm, tn, bk in ((128, 64, 8, 4, 16), (64, 64, 4, 4, 16), (64, 64, 4, 4, 32),
+                               (128, 128, 8, 8, 16), (128, 128, 8, 8, 8)):
+        for promote, vec in ((0, 1), (1, 0), (0, 0)):
+            out.append((bm, bn, tm, tn, bk, promote, vec))
+    return out
+
+
+def name(c):
+    bm, bn, tm, tn, bk, p, v = c
+    return f"tf_staged_b{bm}x{bn}_t{tm}x{tn}_k{bk}" + ("" if p else "_noprom") + ("" if v else "_novec")
+
+
+def main(shards=16):
+    gen = HERE / "_gen"
+    gen.mkdir(exist_ok=True)
+    cfgs = configs()
+    parts = [cfgs[i::shards] for i in range(shards)]
+    for i, part in enumerate(parts):
+        lines = ['#include "../staged_gemm.hpp"', "", "namespace tfk {", "",
+                 "#ifndef __HIP_DEVICE_COMPILE__  // host registry data", f"extern const KernelEntry kStaged{i}[] = {{"]
+        for c in part:
+            t = ", ".join(str(x) for x in c)
+            lines.append(f"    KernelEntry{{FAM_STAGED, {t}, \"{name(c)}\",")
+            lines.append(f"                reinterpret_cast<const void *>(&staged_gemm_kernel<{t}>),")
+            lines.append(f"                &launch_staged<{t}>, nullptr, StagedGemm<{t}>::LDS_BYTES}},")
+        lines += ["};", f"extern const int kStagedCount{i} = {len(part)};", "#else",
+                  "// Device pass: instantiate the kernels the host table names."]
+        for c in part:
+            t = ", ".join(str(x) for x in c)
+            lines.append(f"template __global__ void staged_gemm_kernel<{t}>(GemmParams);")
+        lines += ["#endif", "", "}  // namespace tfk", ""]
+        text = "\n".join(lines)
+        p = gen / f"staged_{i:02d}.hip"
+        if not p.exists() or p.read_text() != text:
+            p.write_text(text)
+    reg = ['#include <vector>', '', '#include "../tf_kernels.h"', '', 'namespace tfk {', '',
+           'extern const KernelEntry kDirectEntries[];', 'extern const int kDirectCount;']
+    for i in range(shards):
+        reg += [f"extern const KernelEntry kStaged{i}[];", f"extern const int kStagedCount{i};"]
+    reg += ["", "static const std::vector<KernelEntry> &all_entries() {",
+            "  static const std::vector<KernelEntry> v = [] {",
+            "    std::vector<KernelEntry> r(kDirectEntries, kDirectEntries + kDirectCount);"]
+    for i in range(shards):
+        reg.append(f"    r.insert(r.end(), kStaged{i}, kStaged{i} + kStagedCount{i});")
+    reg += ["    return r;", "  }();", "  return v;", "}", "",
+            "const KernelEntry *registry_begin() { return all_entries().data(); }",
+            "const KernelEntry *registry_end() { return all_entries().data() + all_entries().size(); }",
+            "", "}  // namespace tfk", ""]
+    text = "\n".join(reg)
+    p = gen / "registry.hip"
+    if not p.exists() or p.read_text() != text:
+        p.write_text(text)
+    print(f"{len(cfgs)} staged instantiations in {shards} shards")
+
+
+if __name__ == "__main__":
+    main(int(sys.argv[1]) if len(sys.argv) > 1 else 16)

@@ -1,0 +1,271 @@
+// The staged FP32 GEMM family for gfx950 (CDNA4): C = epi(A @ B) on wave64
+// MFMA tiles.  This is the kernel the reference pipeline generates for
+// "tile-k=BK" options (docs/stage8.md:9-30; lib/Transforms/Gpu.cpp:229-316),
+// redesigned for the matrix cores instead of translated:
+//
+//  * Option mapping.  block-tile=BM,BN is the workgroup tile; the workgroup has
+//    (BM/TM)*(BN/TN) threads as in the reference, i.e. that many / 64 waves.
+//    thread-tile=TM,TN gives each lane TM*TN accumulators, so a wave owns an
+//    (8*TM) x (8*TN) output tile built from 32x32 MFMA blocks.
+//  * Math.  v_mfma_f32_32x32x2_f32 with the operands swapped (the B tile feeds
+//    src0, the A tile src1), so each lane's accumulators are 4 consecutive
+//    columns of one output row: the epilogue reads bias with one 128-bit load
+//    and writes C with 128-bit stores.
+//  * K order.  Within a k-chunk of 8, lane half h and MFMA step s take
+//    k = 8*kc + 4*h + s, so every lane's A fragment is 4 consecutive k of one
+//    row (one ds_read_b128) and its B fragment 4 rows of one column.  The sum
+//    order differs from the reference's sequential k; parity is the
+//    reference's own FP64 error bound, which holds for any order
+//    (python/tforge_cpu.py:263-271).
+//  * Staging (promote=1).  A tile [BM][BK+4] and B tile [BK][BN+8] in LDS,
+//    double-buffered: the next slab's global loads are in flight while the
+//    current slab feeds the MFMAs; one barrier per slab.  Row padding makes the
+//    b128 fragment reads and the b32 B reads bank-conflict-free.
+//  * vectorize=1: 128-bit global loads and LDS accesses; vectorize=0: 32-bit.
+//  * promote=0: no LDS; each wave streams its fragments from global memory
+//    (through L2), the reference's "+tiling" rung (bench/stage9_ablation.py:23-28).
+//  * Tile order.  Workgroups are dealt round-robin to the 8 XCDs; with
+//    swizzle=1 the workgroups one XCD receives own a compact block of tiles
+//    (grouped by 4 tile rows), so they share A and B panels in that XCD's L2.
+//  * Shapes must be multiples of (BM, BN, BK): the host pads, as the
+//    reference runner does (runners/gpu/tforge-gpu-bench.cu:214-232).
+#pragma once
+
+#include <type_traits>
+
+#include "epilogue.hpp"
+
+namespace tfk {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ void staged_tile_coords(int gx, int gy, int swizzle, int &tm, int &tn) {
+  int w = blockIdx.y * gx + blockIdx.x;
+  const int total = gx * gy;
+  if (!swizzle) {
+    tm = w / gx;
+    tn = w - tm * gx;
+    return;
+  }
+  constexpr int kXcds = 8;
+  if (total % kXcds == 0) w = (w % kXcds) * (total / kXcds) + w / kXcds;
+  constexpr int kGroup = 4;
+  const int group = w / (kGroup * gx);
+  const int first = group * kGroup;
+  const int rows = min(gy - first, kGroup);
+  const int r = w - group * kGroup * gx;
+  tm = first + r % rows;
+  tn = r / rows;
+}
+
+template <int BM, int BN, int TM, int TN, int BK, int PROMOTE, int VEC>
+struct StagedGemm {
+  static constexpr int NT = (BM / TM) * (BN / TN);
+  static constexpr int WTM = 8 * TM, WTN = 8 * TN;
+  static constexpr int NWM = BM / WTM, NWN = BN / WTN;
+  static constexpr int FM = WTM / 32, FN = WTN / 32;
+  static constexpr int LDA = BK + 4;  // LDS A row stride (floats): odd multiple of 4
+  static constexpr int LDB = BN + 8;  // LDS B row stride (floats)
+  static constexpr int A_ELEMS = BM * LDA, B_ELEMS = BK * LDB;
+  static constexpr int LDS_BYTES = PROMOTE ? 2 * (A_ELEMS + B_ELEMS) * 4 : 0;
+  // Global -> register staging per thread and slab.
+  static constexpr int VW = VEC ? 4 : 1;
+  static constexpr int A_VECS = BM * BK / VW, B_VECS = BK * BN / VW;
+  static constexpr int A_PER = (A_VECS + NT - 1) / NT, B_PER = (B_VECS + NT - 1) / NT;
+
+  static_assert(BM % TM == 0 && BN % TN == 0, "block tile must be a multiple of the thread tile");
+  static_assert(NWM * NWN * 64 == NT, "waves must tile the block");
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be made of 32x32 MFMA blocks");
+  static_assert(BK % 8 == 0, "tile-k must be a multiple of 8");
+  static_assert(NT <= 1024, "at most 1024 threads per workgroup");
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS per workgroup exceeds 160 KB");
+};
+
+template <int BM, int BN, int TM, int TN, int BK, int PROMOTE, int VEC>
+__global__ void __launch_bounds__((BM / TM) * (BN / TN))
+staged_gemm_kernel(GemmParams p) {
+  using G = StagedGemm<BM, BN, TM, TN, BK, PROMOTE, VEC>;
+  constexpr int NT = G::NT, WTM = G::WTM, WTN = G::WTN, NWN = G::NWN, FM = G::FM, FN = G::FN;
+  constexpr int LDA = G::LDA, LDB = G::LDB, VW = G::VW;
+
+  const int tid = threadIdx.y * blockDim.x + threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / NWN, wn = wave - wm * NWN;
+  const int l32 = lane & 31, h = lane >> 5;
+
+  int tile_m, tile_n;
+  staged_tile_coords(gridDim.x, gridDim.y, p.swizzle, tile_m, tile_n);
+  const long m0 = (long)tile_m * BM, n0 = (long)tile_n * BN;
+  const float *__restrict__ A = p.A + m0 * p.lda;
+  const float *__restrict__ B = p.B + n0;
+  const long lda = p.lda, ldb = p.ldb;
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int nk = p.K / BK;
+
+  if constexpr (PROMOTE) {
+    __shared__ __attribute__((aligned(16))) float As[2][G::A_ELEMS];
+    __shared__ __attribute__((aligned(16))) float Bs[2][G::B_ELEMS];
+    using VT = typename std::conditional<VEC, f32x4, float>::type;
+    VT ra[G::A_PER], rb[G::B_PER];
+
+    auto load_slab = [&](int k0) {
+#pragma unroll
+      for (int it = 0; it < G::A_PER; ++it) {
+        const int q = tid + it * NT;
+        if (G::A_VECS % NT == 0 || q < G::A_VECS) {
+          const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
+          ra[it] = *reinterpret_cast<const VT *>(A + r * lda + k0 + c);
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < G::B_PER; ++it) {
+        const int q = tid + it * NT;
+        if (G::B_VECS % NT == 0 || q < G::B_VECS) {
+          const int r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
+          rb[it] = *reinterpret_cast<const VT *>(B + (k0 + r) * ldb + c);
+        }
+      }
+    };
+    auto store_slab = [&](int buf) {
+#pragma unroll
+      for (int it = 0; it < G::A_PER; ++it) {
+        const int q = tid + it * NT;
+        if (G::A_VECS % NT == 0 || q < G::A_VECS) {
+          const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
+          *reinterpret_cast<VT *>(&As[buf][r * LDA + c]) = ra[it];
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < G::B_PER; ++it) {
+        const int q = tid + it * NT;
+        if (G::B_VECS % NT == 0 || q < G::B_VECS) {
+          const int r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
+          *reinterpret_cast<VT *>(&Bs[buf][r * LDB + c]) = rb[it];
+        }
+      }
+    };
+
+    if (nk > 0) {
+      load_slab(0);
+      store_slab(0);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      const bool more = kt + 1 < nk;
+      if (more) load_slab((kt + 1) * BK);
+      const float *as = As[cur] + (wm * WTM + l32) * LDA + 4 * h;
+      const float *bs = Bs[cur] + 4 * h * LDB + wn * WTN + l32;
+#pragma unroll
+      for (int kc = 0; kc < BK / 8; ++kc) {
+        f32x4 af[FM];
+        float bf[FN][4];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const float *src = as + i * 32 * LDA + kc * 8;
+          if constexpr (VEC) {
+            af[i] = *reinterpret_cast<const f32x4 *>(src);
+          } else {
+            af[i].x = src[0];
+            af[i].y = src[1];
+            af[i].z = src[2];
+            af[i].w = src[3];
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int s = 0; s < 4; ++s) bf[j][s] = bs[(kc * 8 + s) * LDB + j * 32];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[j][s], af[i][s], acc[i][j], 0, 0, 0);
+      }
+      if (more) store_slab(cur ^ 1);
+      __syncthreads();
+    }
+  } else {
+    // promote=0: fragments straight from global memory, no LDS, no barriers.
+    const float *ag = A + (long)(wm * WTM + l32) * lda + 4 * h;
+    const float *bg = B + 4 * h * ldb + wn * WTN + l32;
+    for (int kt = 0; kt < nk; ++kt) {
+      const int k0 = kt * BK;
+#pragma unroll
+      for (int kc = 0; kc < BK / 8; ++kc) {
+        f32x4 af[FM];
+        float bf[FN][4];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const float *src = ag + (long)i * 32 * lda + k0 + kc * 8;
+          if constexpr (VEC) {
+            af[i] = *reinterpret_cast<const f32x4 *>(src);
+          } else {
+            af[i].x = src[0];
+            af[i].y = src[1];
+            af[i].z = src[2];
+            af[i].w = src[3];
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int s = 0; s < 4; ++s) bf[j][s] = bg[(long)(k0 + kc * 8 + s) * ldb + j * 32];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[j][s], af[i][s], acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+
+  // Epilogue: lane (l32, h) holds, per 32x32 block and group g, C[m, n..n+3]
+  // with m = row l32 of the block and n = 8*g + 4*h.
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const long m = m0 + wm * WTM + i * 32 + l32;
+    float *crow = p.C + m * p.ldc;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = (int)n0 + wn * WTN + j * 32 + 8 * g + 4 * h;
+        f32x4 v;
+        v.x = acc[i][j][4 * g + 0];
+        v.y = acc[i][j][4 * g + 1];
+        v.z = acc[i][j][4 * g + 2];
+        v.w = acc[i][j][4 * g + 3];
+        v = apply_epi4(v, p.epi, m, n);
+        if constexpr (VEC) {
+          *reinterpret_cast<f32x4 *>(crow + n) = v;
+        } else {
+          crow[n + 0] = v.x;
+          crow[n + 1] = v.y;
+          crow[n + 2] = v.z;
+          crow[n + 3] = v.w;
+        }
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int TM, int TN, int BK, int PROMOTE, int VEC>
+hipError_t launch_staged(const GemmParams &p, dim3 grid, dim3 block, hipStream_t stream) {
+  hipLaunchKernelGGL((staged_gemm_kernel<BM, BN, TM, TN, BK, PROMOTE, VEC>), grid, block, 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace tfk

@@ -1,0 +1,71 @@
+// Kernel-side interface of libtforge_hip: parameter blocks passed by value to
+// the gfx950 kernels, the epilogue op encoding, and the registry of
+// ahead-of-time template instantiations.  Shared by the host runtime
+// (runtime.hip) and the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace tfk {
+
+// Epilogue ops applied in order to each output element after the K reduction.
+// They restate the tforge element ops the reference fuses into the matmul's
+// writeback (lib/Transforms/TileAndFuse.cpp:78-131, "EpilogueIntoProducerInit"):
+//   BIAS      y = y + bias[n]          tforge.bias_add (TForgeToLinalg.cpp:113-133)
+//   RELU      y = maximum(y, +0.0)     tforge.relu, IEEE-754-2019 maximum
+//   ADD       y = y + R[m, n]          tforge.add with another buffer
+//   ADD_SELF  y = y + y                tforge.add %v, %v
+enum EpiKind : int { EPI_NONE = 0, EPI_BIAS = 1, EPI_RELU = 2, EPI_ADD = 3, EPI_ADD_SELF = 4 };
+constexpr int kMaxEpi = 4;
+
+struct EpiParams {
+  int nops;
+  int kind[kMaxEpi];
+  const float *ptr[kMaxEpi];  // bias: length-N vector; add: M x N matrix with row stride ldr[i]
+  long ldr[kMaxEpi];
+};
+
+// C[M x N] = epi(A[M x K] @ B[K x N]); row-major, leading dimensions in elements.
+struct GemmParams {
+  const float *A;
+  const float *B;
+  float *C;
+  int M, N, K;
+  long lda, ldb, ldc;
+  EpiParams epi;
+  int swizzle;  // 1: XCD-aware workgroup -> tile order (staged family only)
+};
+
+// Y[M x N] = epi(X[M x N]) for element-op-only programs.
+struct EltParams {
+  const float *X;
+  float *Y;
+  int M, N;
+  long ldx, ldy;
+  EpiParams epi;
+};
+
+enum Family : int { FAM_DIRECT = 0, FAM_STAGED = 1, FAM_ELEMENTWISE = 2 };
+
+using GemmLauncher = hipError_t (*)(const GemmParams &, dim3 grid, dim3 block, hipStream_t);
+using EltLauncher = hipError_t (*)(const EltParams &, dim3 grid, dim3 block, hipStream_t);
+
+// One ahead-of-time instantiation of a kernel template.
+struct KernelEntry {
+  int family;
+  int bm, bn, tm, tn, bk;  // staged: full config; direct/elementwise: tm, tn only (bm = bn = bk = 0)
+  int promote, vectorize;
+  const char *name;
+  const void *fn;  // the __global__ function, for hipFuncGetAttributes / occupancy
+  GemmLauncher gemm;
+  EltLauncher elt;
+  int lds_bytes;   // static LDS of the instantiation
+};
+
+// Registry (defined in the generated registry translation unit).
+const KernelEntry *registry_begin();
+const KernelEntry *registry_end();
+
+}  // namespace tfk

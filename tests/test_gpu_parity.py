@@ -1,0 +1,176 @@
+"""GPU parity: libtforge_hip's kernels on cuda:0 against the CPU oracle.
+
+Bars (python/tforge_gpu.py:112-145):
+  * staged MFMA kernels: err/bound <= 1 against the FP64 reference with the
+    reference's gamma_{K+1} bound, no NaN (outputs are NaN-prefilled), and
+    exact ReLU masks wherever |pre-activation| exceeds the bound;
+  * direct kernels: bit-identical to the sequential-FMA closed form (the
+    reference's naive kernel arithmetic);
+  * element-op programs: bit-exact against the oracle's IEEE ops.
+Every call goes through the C ABI (tf_compile / tf_run / tf_launch).
+"""
+
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+from tensorforge_amd import _lib
+from tensorforge_amd import costmodel as cm
+from tensorforge_amd import tforge_cpu as tc
+from tensorforge_amd import tforge_gpu as tg
+
+pytestmark = pytest.mark.gpu
+
+STAGED = "block-tile={},{} thread-tile={},{} tile-k={} promote=1 vectorize=1"
+
+
+def run_prog(workload, m, n, k, options, ins=None, logical=None):
+    pm, pn, pk = (m, n, k) if logical is None else logical
+    ins = ins or o.make_inputs(workload, m, n, k)
+    kern = _lib.Kernel(tc.gen_mlir(workload, pm, pn, pk if k else None), options, "t.mlir")
+    out = np.empty((m, n), np.float32)
+    lg = None if logical is None or tuple(logical) == (m, n, k) else (m, n, k)
+    kern.run([np.ascontiguousarray(v) for v in ins.values()], out, logical=lg)
+    return ins, out
+
+
+def assert_bound(workload, ins, out):
+    ref, bound = o.fp64_reference(workload, ins)
+    assert not np.isnan(out).any(), "unwritten (NaN-prefilled) outputs"
+    eob = o.e1_metrics(out, ref, bound)["max_err_over_bound"]
+    assert eob <= 1.0, eob
+    if workload == "mbr":
+        assert o.mask_mismatches(out, o.preactivation64(ins), bound) == 0
+    return eob
+
+
+@pytest.mark.parametrize("workload", ["mbr", "matmul"])
+@pytest.mark.parametrize("shape", [(256, 256, 128), (67, 17, 33), (777, 1111, 333), (1, 1, 1), (64, 300, 5)])
+@pytest.mark.parametrize("tt", [(1, 1), (2, 2), (4, 4), (8, 4)])
+def test_direct_bitwise_fma(workload, shape, tt):
+    m, n, k = shape
+    tm, tn = tt
+    opts = f"block-tile={16 * tm},{16 * tn} thread-tile={tm},{tn}"
+    ins, out = run_prog(workload, m, n, k, opts)
+    want = o.matmul_fma(ins["a"], ins["b"])
+    if workload == "mbr":
+        want = o.epilogue(want, ins["bias"], relu=True)
+    assert o.bitwise_diff(out, want) == 0
+
+
+@pytest.mark.parametrize("workload", ["mbr", "matmul"])
+@pytest.mark.parametrize("cfg", [(128, 128, 8, 8, 32), (128, 64, 8, 4, 16), (64, 64, 4, 4, 16), (32, 32, 4, 4, 8),
+                                 (256, 128, 8, 8, 32), (64, 128, 8, 4, 32), (128, 128, 4, 4, 64)])
+@pytest.mark.parametrize("shape", [(256, 256, 128), (512, 256, 1024)])
+def test_staged_bound(workload, cfg, shape):
+    m, n, k = shape
+    pm, pn, pk = cm.padded(cfg, m, n, k)
+    ins, out = run_prog(workload, m, n, k, STAGED.format(*cfg), logical=(pm, pn, pk))
+    assert_bound(workload, ins, out)
+
+
+@pytest.mark.parametrize("workload", ["mbr", "matmul"])
+def test_staged_padded_ragged(workload):
+    """777x1111x333 compiled at the padded 896x1152x336 (reference
+    docs/stage8.md:107); the library pads and unpads."""
+    m, n, k = 777, 1111, 333
+    cfg = (128, 64, 8, 4, 16)
+    ins, out = run_prog(workload, m, n, k, STAGED.format(*cfg), logical=cm.padded(cfg, m, n, k))
+    assert_bound(workload, ins, out)
+
+
+def test_every_staged_instantiation():
+    """Each ahead-of-time instantiation (all promote / vectorize variants) on
+    a small problem padded to its tiles."""
+    ins_cache = {}
+    failures = []
+    for e in _lib.registry():
+        if e["family"] != "staged":
+            continue
+        bm, bn, tm, tn, bk, p, v = e["cfg"]
+        m, n, k = 2 * bm, 2 * bn, 2 * bk if bk >= 32 else 64
+        key = (m, n, k)
+        if key not in ins_cache:
+            ins = o.make_inputs("mbr", m, n, k)
+            ins_cache[key] = (ins,) + o.fp64_reference("mbr", ins)
+        ins, ref, bound = ins_cache[key]
+        opts = f"block-tile={bm},{bn} thread-tile={tm},{tn} tile-k={bk} promote={p} vectorize={v}"
+        print(f"instantiation {e['name']} at {m}x{n}x{k}", flush=True)
+        _, out = run_prog("mbr", m, n, k, opts, ins=ins)
+        eob = o.e1_metrics(out, ref, bound)["max_err_over_bound"]
+        if np.isnan(out).any() or eob > 1.0:
+            failures.append((e["name"], eob))
+    assert not failures, failures
+
+
+@pytest.mark.parametrize("opts", ["", STAGED.format(128, 128, 8, 8, 32)])
+def test_headline_2048(opts):
+    """The headline shape through the product's check() (reference bound)."""
+    d, launch = tg.compile_kernel("mbr", 2048, 2048, 2048, opts or "block-tile=16,16 thread-tile=1,1", tag="test")
+    res, out = tg.check("mbr", 2048, 2048, 2048, d, launch)
+    assert res["pass"], res
+    assert res["err_over_bound"] < 0.05
+
+
+@pytest.mark.parametrize("workload,shape", [("relu", (999, 1001)), ("bias_add", (33, 17)), ("add", (1024, 1024))])
+def test_elementwise_bit_exact(workload, shape):
+    m, n = shape
+    d, launch = tg.compile_kernel(workload, m, n, None, "block-tile=16,16 thread-tile=1,1", tag="test")
+    res, out = tg.check(workload, m, n, None, d, launch)
+    assert res["pass"], res
+
+
+def test_launch_abi_matches_run():
+    """tf_launch on caller-owned device buffers (torch) gives the same bits as tf_run."""
+    import torch
+    m = n = k = 512
+    opts = STAGED.format(128, 128, 8, 8, 32)
+    ins, out = run_prog("mbr", m, n, k, opts)
+    dev = torch.device("cuda:0")
+    bufs = [torch.from_numpy(v).to(dev) for v in ins.values()]
+    c = torch.full((m, n), float("nan"), device=dev)
+    kern = _lib.Kernel(tc.gen_mlir("mbr", m, n, k), opts, "t.mlir")
+    stream = torch.cuda.current_stream()
+    kern.launch([b.data_ptr() for b in bufs] + [c.data_ptr()], stream.cuda_stream)
+    torch.cuda.synchronize()
+    assert o.bitwise_diff(c.cpu().numpy(), out) == 0
+
+
+def test_deterministic():
+    opts = STAGED.format(128, 64, 8, 4, 16)
+    _, a = run_prog("mbr", 512, 512, 512, opts)
+    _, b = run_prog("mbr", 512, 512, 512, opts)
+    assert o.bitwise_diff(a, b) == 0
+
+
+def test_unfused_program_matches_fused_bits():
+    """fuse-elementwise=0 runs matmul, bias_add and relu as three launches;
+    with the direct kernel both are the same FMA chain + IEEE ops."""
+    m, n, k = 300, 200, 100
+    ins = o.make_inputs("mbr", m, n, k)
+    _, fused = run_prog("mbr", m, n, k, "block-tile=16,16 thread-tile=1,1", ins=ins)
+    _, unfused = run_prog("mbr", m, n, k, "block-tile=16,16 thread-tile=1,1 fuse-elementwise=0", ins=ins)
+    assert o.bitwise_diff(fused, unfused) == 0
+
+
+def test_blas_mode_bound():
+    res, out = tg.check("mbr", 1000, 1000, 1000, mode="cublas")
+    assert res["pass"], res
+
+
+def test_resmlp_small():
+    m, n, k = 256, 128, 512
+    d, launch = tg.compile_kernel("resmlp", m, n, k, STAGED.format(128, 128, 8, 8, 32), tag="test")
+    assert len(launch["launches"]) == 2
+    res, out = tg.check("resmlp", m, n, k, d, launch)
+    assert res["pass"], res
+
+
+def test_info_and_bench_keys():
+    d, launch = tg.compile_kernel("mbr", 1024, 1024, 1024, STAGED.format(128, 128, 8, 8, 32), tag="test")
+    inf = tg.info("mbr", 1024, 1024, 1024, d, launch)
+    assert inf["threads"] == 256 and inf["blocks_per_sm"] >= 1
+    r = tg.bench("mbr", 1024, 1024, 1024, d, launch, warmup=2, reps=5)
+    for key in ("gpu", "median_ms", "min_ms", "std_ms", "sm_clock_median_mhz", "padded", "grid", "block"):
+        assert key in r
+    assert r["median_ms"] > 0
