@@ -79,6 +79,15 @@ def lib():
         if not LIB_PATH.exists():
             raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m tensorforge_amd.build` "
                                "(the gfx950 kernels are the only execution path)")
+        # One HIP runtime per process: PyTorch wheels ship their own
+        # libamdhip64.so.7 / libhsa-runtime64.so.1.  Loading torch first makes
+        # this library bind to that already-loaded runtime (same sonames);
+        # loading this library first would leave torch with a second runtime
+        # that cannot open the GPU.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = ctypes.CDLL(str(LIB_PATH))
         for name, res, args in SIGNATURES:
             fn = getattr(L, name)

@@ -1,0 +1,116 @@
+#!/usr/bin/env python3
+"""GPU correctness + timing driver for TensorForge kernels on MI355X (and rocBLAS).
+
+Same command line, shapes and CSV rows as the reference's bench/gpu_bench.py
+(bench/gpu_bench.py:1-103).  Every (variant, workload, shape) is compiled and
+checked before timing:
+  - pass/fail: FP64 reference with the gamma_{K+1} bound (and exact ReLU masks)
+  - reported: max |kernel - rocBLAS| on the same inputs
+Timing: 10 warm-up + 100 reps (HIP events), median; GPU clock sampled per rep
+through amdsmi; clock-adjusted metric = % of the FP32 matrix peak at the median
+clock (256 CUs x 256 FLOP/clk).  --cublas (alias --rocblas) also times rocBLAS
+sgemm plus a separate epilogue kernel, the counterpart of the reference's
+cuBLAS row.
+
+  python -m tensorforge_amd.bench.gpu_bench --csv results/gpu/stage8.csv --tag stage8 \\
+      --variant full-128x128-t8x8-k32="block-tile=128,128 thread-tile=8,8 tile-k=32 promote=1 vectorize=1" \\
+      --cublas
+"""
+
+import argparse
+import sys
+
+import numpy as np
+
+from tensorforge_amd import provenance
+from tensorforge_amd import tforge_gpu as tg
+
+SHAPES = [(256, 256, 256), (512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048),
+          (4096, 4096, 4096), (1000, 1000, 1000), (777, 1111, 333)]
+
+
+def shape_str(m, n, k):
+    return f"{m}x{n}x{k}"
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--csv", required=True)
+    ap.add_argument("--tag", required=True)
+    ap.add_argument("--variant", action="append", default=[])
+    ap.add_argument("--workloads", default="matmul,mbr")
+    ap.add_argument("--shapes", default="")
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--reps", type=int, default=100)
+    ap.add_argument("--flush", action="store_true")
+    ap.add_argument("--cublas", "--rocblas", dest="blas", action="store_true",
+                    help="also time rocBLAS (+ separate epilogue)")
+    ap.add_argument("--check-only", action="store_true")
+    args = ap.parse_args(argv)
+
+    variants = [v.split("=", 1) for v in args.variant]
+    shapes = SHAPES
+    if args.shapes:
+        shapes = [tuple(int(x) for x in s.split("x")) for s in args.shapes.split(",")]
+    base = provenance.common()
+    out = None if args.check_only else provenance.CsvWriter(args.csv)
+    failures = 0
+
+    for workload in args.workloads.split(","):
+        for m, n, k in shapes:
+            flops = 2.0 * m * n * k
+            ref_blas = None
+            if workload in ("matmul", "mbr"):
+                _, ref_blas = tg.check(workload, m, n, k, mode="rocblas")
+            rows = [(name, opts, "kernel") for name, opts in variants]
+            if args.blas and workload in ("matmul", "mbr"):
+                rows.append(("rocblas", "", "rocblas"))
+            for name, opts, mode in rows:
+                kdir = launch = None
+                res_info = {}
+                if mode == "kernel":
+                    kdir, launch = tg.compile_kernel(workload, m, n, k, opts, tag=f"{args.tag}/{name}")
+                    res_info = tg.ptxas_resources(kdir)
+                chk, got = tg.check(workload, m, n, k, kdir, launch, mode)
+                diff = float(np.nanmax(np.abs(got.astype(np.float64) - ref_blas))) if ref_blas is not None else 0.0
+                status = "PASS" if chk["pass"] else "FAIL"
+                print(f"[{status}] {name:>22} {workload:>6} {shape_str(m, n, k):>16} "
+                      f"err/bound={chk['err_over_bound']:.3g} max|x-rocblas|={diff:.3g}", flush=True)
+                if not chk["pass"]:
+                    failures += 1
+                    continue
+                if out is None:
+                    continue
+                r = tg.bench(workload, m, n, k, kdir, launch, mode, args.warmup, args.reps, args.flush)
+                gflops = flops / (r["median_ms"] * 1e-3) / 1e9
+                clk = r["sm_clock_median_mhz"]
+                pct = 100.0 * gflops / tg.fp32_peak_gflops(clk) if clk > 0 else float("nan")
+                pct_nominal = 100.0 * gflops / tg.fp32_peak_gflops(tg.PEAK_CLOCK_MHZ)
+                launch_str = f"grid={r['grid']} block={r['block']} padded={r['padded']}"
+                res = (f"regs={r['regs']} local={r['local_bytes']} smem={r['static_smem']} "
+                       f"blocks/SM={r['blocks_per_sm']} occ={r['theo_occupancy']}")
+                if res_info:
+                    res += (f" spill_st={res_info['spill_stores']} spill_ld={res_info['spill_loads']} "
+                            f"agprs={res_info['agprs']}")
+                pipeline = (f"tforge-gpu-pipeline{{{opts}}}" if mode == "kernel" else
+                            "rocblas_sgemm FP32" + (" + epilogue kernel" if workload == "mbr" else ""))
+                out.row(**base, device=r["gpu"], workload=workload, shape=shape_str(m, n, k),
+                        dtype="f32", pipeline=pipeline, params=f"{name}; {launch_str}; {res}",
+                        threads="", warmup=r["warmup"], reps=r["reps"], median_ms=r["median_ms"],
+                        min_ms=r["min_ms"], std_ms=r["std_ms"], metric="GFLOP/s",
+                        metric_value=gflops, sm_clock_median_mhz=clk,
+                        clock_adjusted_metric=(f"{pct:.2f}% of FP32 matrix peak at median clock; "
+                                               f"{pct_nominal:.2f}% of 157.3 TFLOP/s"),
+                        alloc_bytes_per_call="",
+                        correctness=f"err/bound={chk['err_over_bound']:.3g}; max|x-rocblas|={diff:.3g}",
+                        notes=(f"l2_flush={r['l2_flush']}; gfx clock {r['sm_clock_min_mhz']}-"
+                               f"{r['sm_clock_max_mhz']} MHz; power {r['power_median_w']} W; "
+                               f"hip driver {r['hip_driver']}"))
+                print(f"        median {r['median_ms']:.4f} ms  {gflops:.1f} GFLOP/s  "
+                      f"{pct_nominal:.1f}% of peak ({pct:.1f}% @ {clk:.0f} MHz)  {res}", flush=True)
+    print(f"failures: {failures}")
+    return 1 if failures else 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -75,7 +75,7 @@ def _valid_staged(bm, bn, tm, tn, bk):
     if bm % tm or bn % tn:
         return False
     threads = (bm // tm) * (bn // tn)
-    if threads % 64 or threads > 1024:
+    if threads % 64 or threads > 1024 or threads * tm * tn > 32768:
         return False
     wtm, wtn = 8 * tm, 8 * tn
     if wtm % 32 or wtn % 32 or bm % wtm or bn % wtn or bk % 8:

@@ -29,6 +29,9 @@ def staged_valid(bm, bn, tm, tn, bk, promote=1):
         return f"{threads} threads per block is not a whole number of 64-lane waves"
     if threads > 1024:
         return f"{threads} threads per block exceeds 1024"
+    if threads * tm * tn > 32768:
+        return (f"{threads} threads x {tm * tn} accumulators per lane exceed the register file "
+                "(512 VGPRs per SIMD lane shared by the block's waves)")
     wtm, wtn = 8 * tm, 8 * tn
     if wtm % 32 or wtn % 32:
         return f"wave tile {wtm}x{wtn} (8*TM x 8*TN) is not made of 32x32 MFMA blocks"

@@ -42,6 +42,9 @@ std::string staged_reason(long bm, long bn, long tm, long tn, long bk, bool prom
   const long threads = (bm / tm) * (bn / tn);
   if (threads % 64) return std::to_string(threads) + " threads per block is not a whole number of 64-lane waves";
   if (threads > 1024) return std::to_string(threads) + " threads per block exceeds 1024";
+  if (threads * tm * tn > 32768)
+    return std::to_string(threads) + " threads x " + std::to_string(tm * tn) +
+           " accumulators per lane exceed the register file (512 VGPRs per SIMD lane shared by the block's waves)";
   const long wtm = 8 * tm, wtn = 8 * tn;
   if (wtm % 32 || wtn % 32)
     return "wave tile " + std::to_string(wtm) + "x" + std::to_string(wtn) +

@@ -164,33 +164,44 @@ staged_gemm_kernel(GemmParams p) {
       if (more) load_slab((kt + 1) * BK);
       const float *as = As[cur] + (wm * WTM + l32) * LDA + 4 * h;
       const float *bs = Bs[cur] + 4 * h * LDB + wn * WTN + l32;
-#pragma unroll
-      for (int kc = 0; kc < BK / 8; ++kc) {
-        f32x4 af[FM];
-        float bf[FN][4];
+      // Fragments are double-buffered per k-chunk: the LDS reads of chunk
+      // kc+1 are issued before the MFMAs of chunk kc, so their latency is
+      // covered by matrix-core work instead of stalling the wave.
+      f32x4 af[2][FM];
+      float bf[2][FN][4];
+      auto load_frags = [&](int kc, int slot) {
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
           const float *src = as + i * 32 * LDA + kc * 8;
           if constexpr (VEC) {
-            af[i] = *reinterpret_cast<const f32x4 *>(src);
+            af[slot][i] = *reinterpret_cast<const f32x4 *>(src);
           } else {
-            af[i].x = src[0];
-            af[i].y = src[1];
-            af[i].z = src[2];
-            af[i].w = src[3];
+            af[slot][i].x = src[0];
+            af[slot][i].y = src[1];
+            af[slot][i].z = src[2];
+            af[slot][i].w = src[3];
           }
         }
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
-          for (int s = 0; s < 4; ++s) bf[j][s] = bs[(kc * 8 + s) * LDB + j * 32];
+          for (int s = 0; s < 4; ++s) bf[slot][j][s] = bs[(kc * 8 + s) * LDB + j * 32];
+      };
+      load_frags(0, 0);
+#pragma unroll
+      for (int kc = 0; kc < BK / 8; ++kc) {
+        const int fs = kc & 1;
+        if (kc + 1 < BK / 8) load_frags(kc + 1, fs ^ 1);
+        // Keep the next chunk's LDS reads ahead of this chunk's MFMAs (the
+        // scheduler would otherwise sink them next to their first use).
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
           for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[j][s], af[i][s], acc[i][j], 0, 0, 0);
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[fs][j][s], af[fs][i][s], acc[i][j], 0, 0, 0);
       }
       if (more) store_slab(cur ^ 1);
       __syncthreads();

@@ -1,0 +1,71 @@
+"""The cost model: the reference formula restated exactly (pinned by the
+reference's own Stage 9 result rows), and the CDNA4 retarget's invariants."""
+
+import json
+import pathlib
+
+import pytest
+
+from tensorforge_amd import costmodel as cm
+
+GOLDEN = json.loads((pathlib.Path(__file__).resolve().parent / "golden" / "stage9_costmodel.json").read_text())
+ROWS = [dict(zip(GOLDEN["columns"], r)) for r in GOLDEN["rows"]]
+
+
+def test_reference_formula_reproduces_stage9_rows():
+    """Every 4th row of results/gpu/stage9_autotune.csv (RTX PRO 6000, 188
+    SMs) and e2_a6000_autotune.csv (A6000, 84 SMs, 768 GB/s): pred_ms to the
+    printed 4 decimals and every printed model term."""
+    assert len(ROWS) == 420
+    for r in ROWS:
+        t = cm.Target("ref", "simt", r["sms"], 2280.0, r["dram_bw"])
+        p = cm.predict(tuple(r["cfg"]), r["padded"], {"blocks_per_sm": r["blocks_per_sm"]}, target=t)
+        assert f"{p['pred_ms']:.4f}" == f"{r['pred_ms']:.4f}", r
+        assert (p["waves"], p["resident"], p["bound"]) == (r["waves"], r["resident"], r["bound"]), r
+        assert f"{p['fma_step']:.0f}" == f"{r['fma_step']:.0f}" and f"{p['lds_step']:.0f}" == f"{r['lds_step']:.0f}"
+        assert int(p["latency_exposed"]) == r["latency_exposed"]
+
+
+def test_planted_wrong_latency_breaks_pin():
+    t = cm.Target("ref", "simt", 188, 2280.0, 1530e9, latency=500.0)
+    bad = sum(f"{cm.predict(tuple(r['cfg']), r['padded'], {'blocks_per_sm': r['blocks_per_sm']}, target=t)['pred_ms']:.4f}"
+              != f"{r['pred_ms']:.4f}" for r in ROWS if r["sms"] == 188)
+    assert bad > 0
+
+
+def test_reference_space_has_105_configs():
+    assert len(cm.reference_space()) == 105
+
+
+def test_cdna4_space_is_whole_mfma_waves():
+    space = cm.config_space()
+    assert len(space) > 100
+    for bm, bn, tm, tn, bk in space:
+        threads = (bm // tm) * (bn // tn)
+        assert threads % 64 == 0 and threads <= 1024
+        assert bm % (8 * tm) == 0 and bn % (8 * tn) == 0 and bk % 8 == 0
+        assert 2 * (bm * (bk + 4) + bk * (bn + 8)) * 4 <= 160 * 1024
+
+
+@pytest.mark.parametrize("shape", [(2048, 2048, 2048), (8192, 1024, 4096), (64, 4096, 4096), (4096, 4096, 256)])
+def test_cdna4_model_picks_a_valid_config(shape):
+    cfg = cm.default_config(*shape)
+    assert cfg in cm.config_space()
+    p = cm.predict(cfg, cm.padded(cfg, *shape), cm.estimate_info(cfg))
+    m, n, k = shape
+    # never faster than the FP32 matrix peak
+    assert p["pred_ms"] * 1e-3 >= 2.0 * m * n * k / (256 * 256 * 2.4e9) * 0.999
+
+
+def test_cdna4_model_monotonic_in_k():
+    cfg = (128, 128, 4, 4, 64)
+    inf = {"blocks_per_sm": 1}
+    ts = [cm.predict(cfg, (2048, 2048, k), inf)["pred_ms"] for k in (512, 1024, 2048, 4096)]
+    assert ts == sorted(ts)
+
+
+def test_more_waves_per_simd_hide_the_barrier():
+    # same tile, 16 waves (4 per SIMD) vs 4 waves (1 per SIMD): the barrier term shrinks
+    a = cm.predict((128, 128, 4, 4, 32), (2048, 2048, 2048), {"blocks_per_sm": 1})
+    b = cm.predict((128, 128, 8, 8, 32), (2048, 2048, 2048), {"blocks_per_sm": 1})
+    assert a["waves_per_simd"] == 4 and b["waves_per_simd"] == 1

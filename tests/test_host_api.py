@@ -1,0 +1,114 @@
+"""Host-side API of the Python mirror (python/tforge_gpu.py, python/tforge_cpu.py,
+python/provenance.py) on the CPU: programs, seeded inputs, padding, the FP64
+bound check and its failure modes, artifacts, CSV schema."""
+
+import json
+
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+from tensorforge_amd import provenance
+from tensorforge_amd import tforge_cpu as tc
+from tensorforge_amd import tforge_gpu as tg
+
+
+@pytest.mark.parametrize("workload", ["add", "relu", "bias_add", "matmul", "mbr"])
+def test_make_inputs_match_oracle(workload):
+    a = tc.make_inputs(workload, 33, 17, 9)
+    b = o.make_inputs(workload, 33, 17, 9)
+    assert list(a) == list(b)
+    for k in a:
+        assert a[k].dtype == np.float32 and np.array_equal(a[k], b[k])
+
+
+def test_resmlp_inputs_distribution():
+    ins = tc.make_inputs("resmlp", 512, 256, 1024)
+    assert list(ins) == ["x", "w1", "b1", "w2", "b2"]
+    assert abs(ins["x"].std() - 1.0) < 0.02
+    assert abs(ins["w1"].std() - 1 / 16) < 0.002 and abs(ins["w2"].std() - 1 / 32) < 0.001
+    assert abs(ins["b1"].std() - 0.02) < 0.003
+
+
+def test_padded_shape():
+    opts = "block-tile=128,64 thread-tile=8,4 tile-k=16 promote=1 vectorize=1"
+    assert tg.padded_shape(777, 1111, 333, opts) == (896, 1152, 336)  # docs/stage8.md:107
+    assert tg.padded_shape(777, 1111, 333, "block-tile=16,16 thread-tile=1,1") == (777, 1111, 333)
+
+
+def test_peak():
+    assert abs(tg.FP32_PEAK_TFLOPS - 157.3) < 0.05
+
+
+def test_bound_check_passes_fma_closed_form_with_reference_value():
+    ins = tc.make_inputs("mbr", 256, 256, 256)
+    out = o.mbr_fma(ins["a"], ins["b"], ins["bias"])
+    res = tg._bound_check("mbr", ins, out, 256)
+    assert res["pass"] and f"{res['err_over_bound']:.3g}" == "0.0129"  # results/numerics/e1.csv:7
+    assert res["mask_mismatches"] == 0
+
+
+def test_bound_check_failure_modes():
+    ins = tc.make_inputs("mbr", 64, 64, 64)
+    good = o.mbr_fma(ins["a"], ins["b"], ins["bias"])
+    bad = good.copy()
+    bad[3, 5] = np.nextafter(bad[3, 5], np.float32(np.inf)) + 1e-3  # one element beyond the bound
+    assert not tg._bound_check("mbr", ins, bad, 64)["pass"]
+    nan = good.copy()
+    nan[0, 0] = np.nan  # an unwritten (NaN-prefilled) output
+    r = tg._bound_check("mbr", ins, nan, 64)
+    assert not r["pass"] and r["nan_count"] == 1
+    z = o.preactivation64(ins)
+    i, j = np.unravel_index(np.argmax(z), z.shape)
+    masked = good.copy()
+    masked[i, j] = 0.0  # a clearly positive pre-activation reported as zero
+    r = tg._bound_check("mbr", ins, masked, 64)
+    assert not r["pass"] and r["mask_mismatches"] == 1
+
+
+def test_resmlp_bound_accepts_f32_emulation_and_rejects_errors():
+    m, n, k = 64, 32, 128
+    ins = tc.make_inputs("resmlp", m, n, k)
+    h = o.epilogue(o.matmul_fma(ins["x"], ins["w1"]), ins["b1"], relu=True)
+    y = o.epilogue(o.matmul_fma(h, ins["w2"]), ins["b2"], relu=True, resid=ins["x"])
+    r = tg._resmlp_check(ins, y)
+    assert r["pass"], r
+    y_nofma = o.epilogue(o.epilogue(o.matmul_nofma(o.epilogue(o.matmul_nofma(ins["x"], ins["w1"]), ins["b1"], relu=True),
+                                                   ins["w2"]), ins["b2"], relu=True), resid=ins["x"])
+    assert tg._resmlp_check(ins, y_nofma)["pass"]
+    wrong = o.epilogue(o.matmul_fma(h, ins["w2"]), ins["b2"], relu=True)  # residual add dropped
+    assert not tg._resmlp_check(ins, wrong)["pass"]
+
+
+def test_compile_kernel_writes_artifacts(tmp_path, monkeypatch):
+    monkeypatch.setattr(tg, "ART", tmp_path)
+    d, launch = tg.compile_kernel("mbr", 777, 1111, 333,
+                                  "block-tile=128,64 thread-tile=8,4 tile-k=16 promote=1 vectorize=1", tag="t")
+    assert (d / "input.mlir").read_text() == tc.gen_mlir("mbr", 896, 1152, 336)
+    assert tg.parse_launch(d) == launch == json.loads((d / "launch.json").read_text())
+    assert launch["grid"] == [18, 7, 1] and launch["padded"] == [896, 1152, 336]
+    res = tg.ptxas_resources(d)
+    assert res["regs"] > 0 and res["spill_stores"] == 0 and res["smem"] > 0
+
+
+def test_compile_kernel_error_is_runtime_error(tmp_path, monkeypatch):
+    monkeypatch.setattr(tg, "ART", tmp_path)
+    with pytest.raises(RuntimeError, match="block-tile and thread-tile need 2 values"):
+        tg.compile_kernel("mbr", 64, 64, 64, "block-tile=64")
+
+
+def test_provenance_fields_are_the_reference_schema(tmp_path):
+    assert provenance.FIELDS == [
+        "commit", "mlir_llvm_version", "cuda_version", "device", "job_id", "date",
+        "workload", "shape", "dtype", "pipeline", "params", "threads", "warmup", "reps",
+        "median_ms", "min_ms", "std_ms", "metric", "metric_value", "sm_clock_median_mhz",
+        "clock_adjusted_metric", "alloc_bytes_per_call", "correctness", "notes"]
+    w = provenance.CsvWriter(tmp_path / "x.csv")
+    w.row(commit="c", workload="mbr")
+    with pytest.raises(KeyError):
+        w.row(bogus=1)
+
+
+def test_flops_convention():
+    assert tc.flops_or_bytes("mbr", 2048, 2048, 2048) == ("GFLOP/s", 2.0 * 2048 ** 3)
+    assert tc.flops_or_bytes("resmlp", 4096, 2048, 8192)[1] == 4.0 * 4096 * 2048 * 8192
