@@ -693,8 +693,10 @@ int tf_bench(tf_kernel_t *k, int mode, const long long *logical_mnk, const float
     float t = 0;
     TF_HIP(hipEventElapsedTime(&t, e0, e1));
     ms[i] = t;
+    // Sampled after the rep's event completes; a reading under 500 MHz is the
+    // GPU already dropping to its idle state, not the clock the rep ran at.
     const double c = s.clock_mhz(), p = s.power_w();
-    if (c > 0) clk.push_back(c);
+    if (c >= 500) clk.push_back(c);
     if (p > 0) pwr.push_back(p);
   }
   TF_HIP(hipGetLastError());
