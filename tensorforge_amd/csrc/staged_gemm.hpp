@@ -18,8 +18,10 @@
 //    reference's own FP64 error bound, which holds for any order
 //    (python/tforge_cpu.py:263-271).
 //  * Staging (promote=1).  A tile [BM][BK+4] and B tile [BK][BN+8] in LDS,
-//    double-buffered: the next slab's global loads are in flight while the
-//    current slab feeds the MFMAs; one barrier per slab.  Row padding makes the
+//    double-buffered, one barrier per slab.  Global loads run 1.5 slabs
+//    ahead, the next slab is written to LDS in the middle of the current one
+//    (overlapping MFMAs), and the barrier sits before the slab's last chunk so
+//    those MFMAs hide the next slab's first LDS reads.  Row padding makes the
 //    b128 fragment reads and the b32 B reads bank-conflict-free.
 //  * vectorize=1: 128-bit global loads and LDS accesses; vectorize=0: 32-bit.
 //  * promote=0: no LDS; each wave streams its fragments from global memory
@@ -153,47 +155,68 @@ staged_gemm_kernel(GemmParams p) {
       }
     };
 
+    // Schedule per slab t (slab t lives in buffer t & 1, C = BK / 8 chunks):
+    //   chunk kc:     read chunk kc+1's fragments, then chunk kc's MFMAs
+    //   chunk C/2-1:  after its MFMAs, store slab t+1 (registers, loaded one
+    //                 slab earlier) into the other buffer and issue the global
+    //                 loads of slab t+2 -- the LDS writes overlap matrix work
+    //   chunk C-1:    barrier first (every wave has its last fragments of
+    //                 slab t in registers and its slab t+1 stores done), then
+    //                 read slab t+1's first fragments while the last MFMAs of
+    //                 slab t run.
+    // Hazards: buffer (t+1)&1 held slab t-1, whose last reads precede the
+    // barrier of slab t-1; slab t+1's stores precede the barrier of slab t,
+    // which precedes every read of it.
+    // MID < C - 1 whenever C >= 2, so slab t+1's stores always precede the
+    // barrier at chunk C-1; with a single chunk they are issued before it.
+    constexpr int C = BK / 8, MID = C >= 2 ? C / 2 - 1 : 0;
+    f32x4 af[2][FM];
+    float bf[2][FN][4];
+    auto load_frags = [&](int buf, int kc, int slot) {
+      const float *as = As[buf] + (wm * WTM + l32) * LDA + 4 * h + kc * 8;
+      const float *bs = Bs[buf] + (4 * h + kc * 8) * LDB + wn * WTN + l32;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const float *src = as + i * 32 * LDA;
+        if constexpr (VEC) {
+          af[slot][i] = *reinterpret_cast<const f32x4 *>(src);
+        } else {
+          af[slot][i].x = src[0];
+          af[slot][i].y = src[1];
+          af[slot][i].z = src[2];
+          af[slot][i].w = src[3];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) bf[slot][j][s] = bs[s * LDB + j * 32];
+    };
     if (nk > 0) {
       load_slab(0);
       store_slab(0);
+      if (nk > 1) load_slab(BK);
     }
     __syncthreads();
+    if (nk > 0) load_frags(0, 0, 0);
     for (int kt = 0; kt < nk; ++kt) {
       const int cur = kt & 1;
       const bool more = kt + 1 < nk;
-      if (more) load_slab((kt + 1) * BK);
-      const float *as = As[cur] + (wm * WTM + l32) * LDA + 4 * h;
-      const float *bs = Bs[cur] + 4 * h * LDB + wn * WTN + l32;
-      // Fragments are double-buffered per k-chunk: the LDS reads of chunk
-      // kc+1 are issued before the MFMAs of chunk kc, so their latency is
-      // covered by matrix-core work instead of stalling the wave.
-      f32x4 af[2][FM];
-      float bf[2][FN][4];
-      auto load_frags = [&](int kc, int slot) {
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
-          const float *src = as + i * 32 * LDA + kc * 8;
-          if constexpr (VEC) {
-            af[slot][i] = *reinterpret_cast<const f32x4 *>(src);
-          } else {
-            af[slot][i].x = src[0];
-            af[slot][i].y = src[1];
-            af[slot][i].z = src[2];
-            af[slot][i].w = src[3];
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-          for (int s = 0; s < 4; ++s) bf[slot][j][s] = bs[(kc * 8 + s) * LDB + j * 32];
-      };
-      load_frags(0, 0);
-#pragma unroll
-      for (int kc = 0; kc < BK / 8; ++kc) {
+      for (int kc = 0; kc < C; ++kc) {
         const int fs = kc & 1;
-        if (kc + 1 < BK / 8) load_frags(kc + 1, fs ^ 1);
-        // Keep the next chunk's LDS reads ahead of this chunk's MFMAs (the
-        // scheduler would otherwise sink them next to their first use).
+        if (C == 1 && more) {
+          store_slab(cur ^ 1);
+          if (kt + 2 < nk) load_slab((kt + 2) * BK);
+        }
+        if (kc + 1 < C) {
+          load_frags(cur, kc + 1, fs ^ 1);
+        } else if (more) {
+          __syncthreads();
+          load_frags(cur ^ 1, 0, fs ^ 1);
+        }
+        // Keep the fragment reads (and the barrier) ahead of this chunk's
+        // MFMAs: the scheduler would otherwise sink the reads to their use.
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < 4; ++s)
@@ -202,9 +225,22 @@ staged_gemm_kernel(GemmParams p) {
 #pragma unroll
             for (int j = 0; j < FN; ++j)
               acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[fs][j][s], af[fs][i][s], acc[i][j], 0, 0, 0);
+        if (C >= 2 && kc == MID && more) {
+          __builtin_amdgcn_sched_barrier(0);
+          store_slab(cur ^ 1);
+          if (kt + 2 < nk) load_slab((kt + 2) * BK);
+        }
       }
-      if (more) store_slab(cur ^ 1);
-      __syncthreads();
+      // With an odd chunk count the next slab's first fragments landed in
+      // slot 1; the loop expects them in slot 0.
+      if constexpr (C % 2 == 1) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) af[0][i] = af[1][i];
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int s = 0; s < 4; ++s) bf[0][j][s] = bf[1][j][s];
+      }
     }
   } else {
     // promote=0: fragments straight from global memory, no LDS, no barriers.
