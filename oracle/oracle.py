@@ -66,6 +66,7 @@ def lib():
         getattr(L, fn).argtypes = [fp, fp, fp, i64, i64, i64, i32]
         getattr(L, fn).restype = None
     L.tfo_epilogue.argtypes = [fp, fp, fp, i64, i64, i32]
+    L.tfo_matmul_scalar_mnk.argtypes = [fp, fp, fp, i64, i64, i64]
     L.tfo_epilogue.restype = None
     L.tfo_add.argtypes = [fp, fp, fp, i64]
     L.tfo_relu.argtypes = [fp, fp, i64]
@@ -119,6 +120,16 @@ def matmul_nofma(a, b, threads=0):
     assert k == k2
     c = np.empty((m, n), np.float32)
     lib().tfo_matmul_nofma(_p(a), _p(b), _p(c), m, n, k, threads)
+    return c
+
+
+def matmul_scalar_mnk(a, b):
+    """tfo_matmul_scalar_mnk: the no-FMA form in the default CPU pipeline's loop order."""
+    a, b = _f32(a), _f32(b)
+    (m, k), (k2, n) = a.shape, b.shape
+    assert k == k2
+    c = np.empty((m, n), np.float32)
+    lib().tfo_matmul_scalar_mnk(_p(a), _p(b), _p(c), m, n, k)
     return c
 
 

@@ -16,6 +16,8 @@
  *  tfo_matmul_nofma  acc = +0.0f; acc = acc + (float)(A[m,k] * B[k,n]), each product
  *                    rounded before the add: the reference's default CPU pipeline
  *                    (cpu-scalar in results/numerics/e1.csv; docs/numerics.md:15).
+ *  tfo_matmul_scalar_mnk  the same arithmetic in the default pipeline's loop
+ *                    order (one output at a time, k innermost), for timing.
  *  tfo_epilogue      y = C + bias[n]  (tforge.bias_add, lib/Conversion/TForgeToLinalg.cpp:113-133)
  *                    y = maximum(y, +0.0)  IEEE-754-2019 maximum: NaN -> NaN,
  *                        -0 -> +0 (tforge.relu, docs/dialect.md:26-30;
@@ -98,6 +100,22 @@ void tfo_matmul_nofma(const float *A, const float *B, float *C, long M, long N, 
       }
     }
   }
+}
+
+/* The same closed form in the reference's default CPU loop order: one output at
+ * a time (m, n outer; k inner, B read down a column), scalar, no FMA
+ * (--tforge-cpu-pipeline defaults; docs/stage4.md:63 times it at ~0.6 GFLOP/s).
+ * Bitwise equal to tfo_matmul_nofma; it exists to time the scalar baseline. */
+void tfo_matmul_scalar_mnk(const float *A, const float *B, float *C, long M, long N, long K) {
+  for (long m = 0; m < M; ++m)
+    for (long n = 0; n < N; ++n) {
+      float acc = 0.0f;
+      for (long k = 0; k < K; ++k) {
+        float p = A[m * K + k] * B[k * N + n];
+        acc = acc + p;
+      }
+      C[m * N + n] = acc;
+    }
 }
 
 void tfo_epilogue(float *C, const float *bias, const float *R, long M, long N, int flags) {
@@ -238,7 +256,7 @@ double tfo_time_mbr_vec6x16(const float *A, const float *B, const float *bias, f
   return reps % 2 ? ts[reps / 2] : 0.5 * (ts[reps / 2 - 1] + ts[reps / 2]);
 }
 
-/* Same for the scalar no-FMA closed form plus its separate epilogue (the
+/* Same for the scalar (m, n, k) no-FMA loop plus its separate epilogue (the
  * reference's default CPU pipeline), 1 thread. */
 double tfo_time_scalar(const float *A, const float *B, const float *bias, float *C, long M,
                        long N, long K, int flags, int warmup, int reps) {
@@ -248,7 +266,7 @@ double tfo_time_scalar(const float *A, const float *B, const float *bias, float 
   for (int i = 0; i < warmup + reps; ++i) {
     struct timespec t0, t1;
     clock_gettime(CLOCK_MONOTONIC, &t0);
-    tfo_matmul_nofma(A, B, C, M, N, K, 1);
+    tfo_matmul_scalar_mnk(A, B, C, M, N, K);
     tfo_epilogue(C, bias, 0, M, N, flags);
     clock_gettime(CLOCK_MONOTONIC, &t1);
     if (i >= warmup) ts[i - warmup] = (t1.tv_sec - t0.tv_sec) * 1e9 + (t1.tv_nsec - t0.tv_nsec);

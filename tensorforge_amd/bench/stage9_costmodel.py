@@ -10,7 +10,8 @@ bench/stage9_costmodel.py:1-155.  For each shape:
   3. autotuner: check (one FP64 reference per shape) and time every
      configuration; the autotuner's pick is the fastest measured,
   4. report the model pick relative to the best, raw and clock-adjusted, the
-     Spearman rank correlation, and record the best configuration in
+     Spearman rank correlation (with --split-k, every configuration is also
+     tried with each split-K factor, a backend option), and record the best configuration in
      tensorforge_amd/tuned_configs.json (read by bench.py and tuned_options()).
 
   python -m tensorforge_amd.bench.stage9_costmodel --shapes 2048x2048x2048 \\
@@ -61,6 +62,8 @@ def main(argv=None):
     ap.add_argument("--reps", type=int, default=100)
     ap.add_argument("--space", choices=("cdna4", "reference"), default="cdna4")
     ap.add_argument("--top", type=int, default=0, help="time only the N best-predicted configurations")
+    ap.add_argument("--split-k", default="1",
+                    help="split-K factors to cross with the configuration grid, e.g. 1,2,4,8 (backend option)")
     ap.add_argument("--tuned", default=str(TUNED), help="JSON table the best configuration is recorded in")
     ap.add_argument("--no-record", action="store_true", help="do not record the best configuration")
     args = ap.parse_args(argv)
@@ -79,9 +82,11 @@ def main(argv=None):
                      "model_pick", "model_pick_ms", "model_pick_pct", "best", "best_ms", "best_pct",
                      "ratio_raw", "ratio_clock_adjusted", "model_rank_of_best", "measured_rank_of_model_pick",
                      "spearman_pred_vs_measured", "model_cost_s", "autotune_cost_s"])
-    space = cm.config_space() if args.space == "cdna4" else cm.reference_space()
+    base_space = cm.config_space() if args.space == "cdna4" else cm.reference_space()
+    split_factors = tuple(int(v) for v in args.split_k.split(","))
     wl = args.workload
     for m, n, k in shapes:
+        space = cm.with_splits(base_space, m, n, k, split_factors)
         tag = f"stage9/{m}x{n}x{k}"
         t0 = time.time()
         compiled, failed = [], []

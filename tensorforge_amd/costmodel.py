@@ -28,6 +28,11 @@ replaces the per-step terms with what bounds the gfx950 MFMA kernel:
   sync       one barrier per slab; its bubble is hidden by other waves on the
              SIMD, so it is divided by q.
 
+Split-K (a backend option, a sixth configuration entry S): S workgroups per
+output tile, each over Kp/S; the tile count is multiplied by S and the K
+steps divided by S, and the reduction launch adds its HBM traffic (S partial
+slices written and read, C written) plus a fixed launch cost.
+
 Constants are AMD's published MI355X figures (256 CUs, 2.4 GHz, FP32 matrix
 256 FLOP/clk/CU, 160 KiB LDS, 8 TB/s HBM); LATENCY and SYNC are assumptions
 calibrated on measurements, and the model only ranks configurations.
@@ -59,6 +64,7 @@ class Target:
     mfma_cycles: float = 64.0           # v_mfma_f32_32x32x2_f32 per wave
     lds_per_cu: int = 160 * 1024
     max_waves_per_simd: int = 8
+    launch_s: float = 3e-6              # mfma: one more dependent kernel launch (split-K reduction)
 
 
 # The reference's model (python/costmodel.py:41-46); TF_GPU_SMS / TF_GPU_DRAM_BW as there.
@@ -111,19 +117,39 @@ def config_space():
     return out
 
 
+def splits_of(cfg):
+    """Split-K factor of a configuration: (BM, BN, TM, TN, BK[, S])."""
+    return cfg[5] if len(cfg) > 5 else 1
+
+
 def options(cfg):
-    bm, bn, tm, tn, bk = cfg
-    return f"block-tile={bm},{bn} thread-tile={tm},{tn} tile-k={bk} promote=1 vectorize=1"
+    bm, bn, tm, tn, bk = cfg[:5]
+    s = splits_of(cfg)
+    return (f"block-tile={bm},{bn} thread-tile={tm},{tn} tile-k={bk} promote=1 vectorize=1"
+            + (f" split-k={s}" if s > 1 else ""))
 
 
 def name(cfg):
-    bm, bn, tm, tn, bk = cfg
-    return f"b{bm}x{bn}-t{tm}x{tn}-k{bk}"
+    bm, bn, tm, tn, bk = cfg[:5]
+    s = splits_of(cfg)
+    return f"b{bm}x{bn}-t{tm}x{tn}-k{bk}" + (f"-s{s}" if s > 1 else "")
 
 
 def kernel_name(cfg):
-    bm, bn, tm, tn, bk = cfg
+    bm, bn, tm, tn, bk = cfg[:5]
     return f"tf_staged_b{bm}x{bn}_t{tm}x{tn}_k{bk}"
+
+
+def with_splits(space, m, n, k, splits=(1, 2, 4, 8, 16)):
+    """Each configuration once per split-K factor that leaves every split at
+    least one K slab (S = 1 keeps the 5-entry form)."""
+    out = []
+    for cfg in space:
+        nk = padded(cfg, m, n, k)[2] // cfg[4]
+        for s in splits:
+            if s <= nk:
+                out.append(tuple(cfg[:5]) if s == 1 else tuple(cfg[:5]) + (s,))
+    return out
 
 
 def _resources():
@@ -135,7 +161,7 @@ def estimate_info(cfg, target=MI355X, resources=None):
     """Blocks per CU without a GPU: the smaller of the register-limited waves
     per SIMD (compiler resource remarks) and the LDS limit; the occupancy API
     (tforge_gpu.info) gives the same number on the device."""
-    bm, bn, tm, tn, bk = cfg
+    bm, bn, tm, tn, bk = cfg[:5]
     threads = (bm // tm) * (bn // tn)
     w = threads // 64
     rec = (resources if resources is not None else _resources()).get(kernel_name(cfg), {})
@@ -150,12 +176,13 @@ def estimate_info(cfg, target=MI355X, resources=None):
 
 def predict(cfg, padded, info, clock_mhz=None, target=MI355X):
     """Predicted time in ms and the terms that produced it."""
-    bm, bn, tm, tn, bk = cfg
+    bm, bn, tm, tn, bk = cfg[:5]
+    splits = splits_of(cfg)
     mp, np_, kp = padded
     clock = clock_mhz or target.clock_mhz
     bps = max(1, info["blocks_per_sm"])
     threads = (bm // tm) * (bn // tn)
-    blocks = (mp // bm) * (np_ // bn)
+    blocks = (mp // bm) * (np_ // bn) * splits
     waves = math.ceil(blocks / (target.units * bps))
     resident = min(bps, math.ceil(blocks / target.units))
     if target.kind == "simt":
@@ -184,10 +211,13 @@ def predict(cfg, padded, info, clock_mhz=None, target=MI355X):
     exposed = max(0.0, target.latency - compute)
     step = compute + exposed + target.sync / q
     epilogue = target.latency + resident * bm * bn * 4 / target.l2_bytes_per_cycle
-    cycles = waves * ((kp // bk) * step + target.latency + epilogue)
+    ksteps = -(-(kp // bk) // splits)
+    cycles = waves * (ksteps * step + target.latency + epilogue)
     t_compute = cycles / (clock * 1e6)
     t_dram = 4.0 * (mp * kp + kp * np_ + mp * np_ + np_) / target.dram_bw
     t = max(t_compute, t_dram)
+    if splits > 1:
+        t += (2 * splits + 1) * 4.0 * mp * np_ / target.dram_bw + target.launch_s
     terms = {"mfma": mfma_step, "lds": lds_step, "l2": l2_step}
     bound = "dram" if t_dram > t_compute else max(terms, key=terms.get)
     return {"pred_ms": t * 1e3, "waves": waves, "resident": resident, "blocks": blocks,
@@ -197,7 +227,7 @@ def predict(cfg, padded, info, clock_mhz=None, target=MI355X):
 
 
 def padded(cfg, m, n, k):
-    bm, bn, _, _, bk = cfg
+    bm, bn, _, _, bk = cfg[:5]
     up = lambda x, t: -(-x // t) * t
     return up(m, bm), up(n, bn), up(k, bk)
 
@@ -215,6 +245,6 @@ def rank(m, n, k, space=None, target=MI355X, infos=None):
 
 
 def default_config(m, n, k):
-    """The cost model's pick for a shape: what the backend uses when no
-    autotuned configuration is recorded."""
-    return rank(m, n, k)[0]
+    """The cost model's pick for a shape, split-K factors included: what the
+    backend uses when no autotuned configuration is recorded."""
+    return rank(m, n, k, space=with_splits(config_space(), m, n, k))[0]

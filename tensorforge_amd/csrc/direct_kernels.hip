@@ -12,6 +12,9 @@
 // alone, or chains of them) run one thread per TM x TN elements with the same
 // launch geometry, one IEEE operation per op, so results are bit-exact against
 // NumPy float32 (python/tforge_gpu.py:116-126).
+//
+// Split-K reduction: the second launch of a staged matmul compiled with
+// split-k=S (a backend option): C = epi(slice 0 + ... + slice S-1).
 #include "epilogue.hpp"
 
 namespace tfk {
@@ -69,6 +72,37 @@ hipError_t launch_direct(const GemmParams &p, dim3 grid, dim3 block, hipStream_t
 template <int TM, int TN>
 hipError_t launch_elementwise(const EltParams &p, dim3 grid, dim3 block, hipStream_t stream) {
   hipLaunchKernelGGL((elementwise_kernel<TM, TN>), grid, block, 0, stream, p);
+  return hipGetLastError();
+}
+
+// Split-K reduction: one thread per 4 consecutive outputs; the partial-sum
+// slices are read 4 at a time (independent loads in flight) and added in
+// slice order, so the result does not depend on scheduling.
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(ReduceParams p) {
+  const long q = (long)blockIdx.x * 256 + threadIdx.x;
+  const long per_row = p.N / 4;
+  if (q >= (long)p.M * per_row) return;
+  const long m = q / per_row;
+  const int n = (int)(q - m * per_row) * 4;
+  const long slice = (long)p.M * p.ldc;
+  const float *src = p.ws + m * p.ldc + n;
+  auto ld = [&](int s) { return *reinterpret_cast<const f32x4 *>(src + s * slice); };
+  f32x4 v = ld(0);
+  int s = 1;
+  for (; s + 4 <= p.splits; s += 4) {
+    const f32x4 t0 = ld(s), t1 = ld(s + 1), t2 = ld(s + 2), t3 = ld(s + 3);
+    v += t0;
+    v += t1;
+    v += t2;
+    v += t3;
+  }
+  for (; s < p.splits; ++s) v += ld(s);
+  *reinterpret_cast<f32x4 *>(p.C + m * p.ldc + n) = apply_epi4(v, p.epi, m, n);
+}
+
+hipError_t launch_splitk_reduce(const ReduceParams &p, hipStream_t stream) {
+  const long quads = (long)p.M * (p.N / 4);
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 

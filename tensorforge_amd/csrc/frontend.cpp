@@ -572,6 +572,11 @@ bool parse_options(const std::string &text, Options &o, std::string &err) {
         err = pipe + "invalid value '" + val + "' for list option '" + key + "'";
         return false;
       }
+    } else if (key == "split-k") {
+      if (!parse_int(val, o.split_k) || o.split_k < 1 || o.split_k > 64) {
+        err = pipe + "invalid value '" + val + "' for option 'split-k' (1 to 64)";
+        return false;
+      }
     } else if (key == "tile-k") {
       if (!parse_int(val, o.tile_k) || o.tile_k < 0) {
         err = pipe + "invalid value '" + val + "' for option 'tile-k'";

@@ -74,10 +74,14 @@ struct tf_kernel {
   std::vector<Launch> launches;
   int device = -1;
   std::vector<void *> inter;  // intermediate device buffers, by buffer id
+  // Split-K partial sums, shared by the stages (they run in stream order).
+  size_t ws_bytes = 0;
+  void *ws = nullptr;
   std::vector<double> samples;
   ~tf_kernel() {
     for (void *p : inter)
       if (p) (void)hipFree(p);
+    if (ws) (void)hipFree(ws);
   }
 };
 
@@ -119,6 +123,18 @@ int select_launches(tf_kernel *k) {
                                                     " threads per block exceeds 1024"));
     L.block = dim3((unsigned)tx, (unsigned)ty, 1);
     L.grid = dim3((unsigned)std::max(1L, ceil_div(st.N, o.bn)), (unsigned)std::max(1L, ceil_div(st.M, o.bm)), 1);
+    if (o.split_k > 1) {
+      if (!staged)
+        return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc,
+                                                  "tforge-gpu-pipeline: split-k needs tile-k"));
+      if (st.K / o.tile_k < o.split_k)
+        return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc,
+                                                  "tforge-gpu-pipeline: split-k " + std::to_string(o.split_k) +
+                                                      " exceeds the " + std::to_string(st.K / o.tile_k) +
+                                                      " K slabs of this matmul"));
+      L.grid.z = (unsigned)o.split_k;
+      k->ws_bytes = std::max(k->ws_bytes, (size_t)o.split_k * st.M * st.N * sizeof(float));
+    }
     k->launches.push_back(L);
   }
   return TF_OK;
@@ -163,7 +179,20 @@ int launch_stage(const tf_kernel *k, size_t s, void *const *ptrs, hipStream_t st
     p.ldc = st.N;
     p.epi = make_epi(st, ptrs);
     p.swizzle = k->opts.xcd_swizzle ? 1 : 0;
+    p.splits = (int)L.grid.z;
+    if (p.splits > 1) p.ws = static_cast<float *>(k->ws);
     err = L.entry->gemm(p, L.grid, L.block, stream);
+    if (err == hipSuccess && p.splits > 1) {
+      tfk::ReduceParams r{};
+      r.ws = p.ws;
+      r.C = p.C;
+      r.M = p.M;
+      r.N = p.N;
+      r.splits = p.splits;
+      r.ldc = p.ldc;
+      r.epi = p.epi;
+      err = tfk::launch_splitk_reduce(r, stream);
+    }
   } else {
     tfk::EltParams p{};
     p.X = static_cast<const float *>(ptrs[st.x]);
@@ -191,12 +220,15 @@ int pointer_table(tf_kernel *k, void *const *bufs, std::vector<void *> &ptrs) {
     for (void *p : k->inter)
       if (p) (void)hipFree(p);
     k->inter.assign(pl.buffers.size(), nullptr);
+    if (k->ws) (void)hipFree(k->ws);
+    k->ws = nullptr;
     k->device = dev;
   }
   for (size_t i = pl.nargs + 1; i < pl.buffers.size(); ++i) {
     if (!k->inter[i]) TF_HIP(hipMalloc(&k->inter[i], std::max<int64_t>(1, pl.buffers[i].numel()) * sizeof(float)));
     ptrs[i] = k->inter[i];
   }
+  if (k->ws_bytes && !k->ws) TF_HIP(hipMalloc(&k->ws, k->ws_bytes));
   return TF_OK;
 }
 

@@ -29,6 +29,11 @@
 //  * Tile order.  Workgroups are dealt round-robin to the 8 XCDs; with
 //    swizzle=1 the workgroups one XCD receives own a compact block of tiles
 //    (grouped by 4 tile rows), so they share A and B panels in that XCD's L2.
+//  * Split-K (an option the reference does not have): gridDim.z workgroups
+//    per output tile, each over a contiguous range of K slabs, so shapes with
+//    few output tiles (64 x 4096 x 4096) still fill 256 CUs.  Partial sums go
+//    to a workspace with ordinary cached stores; a second, HBM-bound kernel
+//    adds them in a fixed order (deterministic) and applies the epilogue.
 //  * Shapes must be multiples of (BM, BN, BK): the host pads, as the
 //    reference runner does (runners/gpu/tforge-gpu-bench.cu:214-232).
 #pragma once
@@ -98,9 +103,13 @@ staged_gemm_kernel(GemmParams p) {
   int tile_m, tile_n;
   staged_tile_coords(gridDim.x, gridDim.y, p.swizzle, tile_m, tile_n);
   const long m0 = (long)tile_m * BM, n0 = (long)tile_n * BN;
-  const float *__restrict__ A = p.A + m0 * p.lda;
-  const float *__restrict__ B = p.B + n0;
   const long lda = p.lda, ldb = p.ldb;
+  // Split-K: workgroup z reduces K slabs [kb, ke).
+  const int splits = p.splits > 1 ? p.splits : 1, split = blockIdx.z;
+  const int kb = (int)((long)(p.K / BK) * split / splits);
+  const int ke = (int)((long)(p.K / BK) * (split + 1) / splits);
+  const float *__restrict__ A = p.A + m0 * lda + (long)kb * BK;
+  const float *__restrict__ B = p.B + n0 + (long)kb * BK * ldb;
 
   f32x16 acc[FM][FN];
 #pragma unroll
@@ -110,7 +119,7 @@ staged_gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  const int nk = p.K / BK;
+  const int nk = ke - kb;
 
   if constexpr (PROMOTE) {
     __shared__ __attribute__((aligned(16))) float As[2][G::A_ELEMS];
@@ -281,21 +290,42 @@ staged_gemm_kernel(GemmParams p) {
 
   // Epilogue: lane (l32, h) holds, per 32x32 block and group g, C[m, n..n+3]
   // with m = row l32 of the block and n = 8*g + 4*h.
+  auto group = [&](int i, int j, int g) {
+    f32x4 v;
+    v.x = acc[i][j][4 * g + 0];
+    v.y = acc[i][j][4 * g + 1];
+    v.z = acc[i][j][4 * g + 2];
+    v.w = acc[i][j][4 * g + 3];
+    return v;
+  };
+  auto row_of = [&](int i) { return m0 + wm * WTM + i * 32 + l32; };
+  auto col_of = [&](int j, int g) { return (int)n0 + wn * WTN + j * 32 + 8 * g + 4 * h; };
+
+  if (splits > 1) {
+    // Split-K: this workgroup's partial sums go to slice `split` of the
+    // workspace; splitk_reduce_kernel, launched next on the same stream, adds
+    // the slices in order and runs the epilogue.
+    float *own = p.ws + split * (long)p.M * p.ldc;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<f32x4 *>(own + row_of(i) * p.ldc + col_of(j, g)) = group(i, j, g);
+    return;
+  }
+
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
-    const long m = m0 + wm * WTM + i * 32 + l32;
+    const long m = row_of(i);
     float *crow = p.C + m * p.ldc;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int n = (int)n0 + wn * WTN + j * 32 + 8 * g + 4 * h;
-        f32x4 v;
-        v.x = acc[i][j][4 * g + 0];
-        v.y = acc[i][j][4 * g + 1];
-        v.z = acc[i][j][4 * g + 2];
-        v.w = acc[i][j][4 * g + 3];
-        v = apply_epi4(v, p.epi, m, n);
+        const int n = col_of(j, g);
+        f32x4 v = apply_epi4(group(i, j, g), p.epi, m, n);
         if constexpr (VEC) {
           *reinterpret_cast<f32x4 *>(crow + n) = v;
         } else {

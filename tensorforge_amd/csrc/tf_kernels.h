@@ -36,6 +36,21 @@ struct GemmParams {
   long lda, ldb, ldc;
   EpiParams epi;
   int swizzle;  // 1: XCD-aware workgroup -> tile order (staged family only)
+  // Split-K (staged family): gridDim.z = splits workgroups per output tile,
+  // each reducing a contiguous range of K slabs into slice z of ws
+  // (splits x M x ldc floats) instead of writing C; launch_splitk_reduce
+  // then forms C = epi(sum of the slices in order 0..splits-1).
+  int splits;
+  float *ws;
+};
+
+// C[M x N] = epi(ws[0] + ws[1] + ... + ws[splits-1]), slices of M x ldc.
+struct ReduceParams {
+  const float *ws;
+  float *C;
+  int M, N, splits;
+  long ldc;
+  EpiParams epi;
 };
 
 // Y[M x N] = epi(X[M x N]) for element-op-only programs.
@@ -63,6 +78,10 @@ struct KernelEntry {
   EltLauncher elt;
   int lds_bytes;   // static LDS of the instantiation
 };
+
+// The split-K reduction (direct_kernels.hip); N and ldc multiples of 4,
+// ws and C 16-byte aligned.
+hipError_t launch_splitk_reduce(const ReduceParams &p, hipStream_t stream);
 
 // Registry (defined in the generated registry translation unit).
 const KernelEntry *registry_begin();

@@ -50,7 +50,7 @@ def test_cdna4_space_is_whole_mfma_waves():
 @pytest.mark.parametrize("shape", [(2048, 2048, 2048), (8192, 1024, 4096), (64, 4096, 4096), (4096, 4096, 256)])
 def test_cdna4_model_picks_a_valid_config(shape):
     cfg = cm.default_config(*shape)
-    assert cfg in cm.config_space()
+    assert cfg[:5] in cm.config_space() and cfg in cm.with_splits(cm.config_space(), *shape)
     p = cm.predict(cfg, cm.padded(cfg, *shape), cm.estimate_info(cfg))
     m, n, k = shape
     # never faster than the FP32 matrix peak
@@ -69,3 +69,29 @@ def test_more_waves_per_simd_hide_the_barrier():
     a = cm.predict((128, 128, 4, 4, 32), (2048, 2048, 2048), {"blocks_per_sm": 1})
     b = cm.predict((128, 128, 8, 8, 32), (2048, 2048, 2048), {"blocks_per_sm": 1})
     assert a["waves_per_simd"] == 4 and b["waves_per_simd"] == 1
+
+
+def test_split_k_configurations():
+    cfg = (64, 128, 4, 4, 32)
+    assert cm.options(cfg + (8,)) == cm.options(cfg) + " split-k=8"
+    assert cm.name(cfg + (8,)) == "b64x128-t4x4-k32-s8" and cm.kernel_name(cfg + (8,)) == cm.kernel_name(cfg)
+    assert cm.options(cfg + (1,)) == cm.options(cfg)
+    # 64 K slabs of 32 at K = 2048: every factor up to 64 fits, 128 does not
+    sp = cm.with_splits([cfg], 64, 4096, 2048, (1, 2, 64, 128))
+    assert sp == [cfg, cfg + (2,), cfg + (64,)]
+
+
+def test_split_k_model_terms():
+    """Splitting K multiplies the workgroups, divides the K steps, and pays
+    the reduction's HBM traffic plus one launch."""
+    cfg, shape = (64, 64, 4, 4, 32), (64, 4096, 4096)
+    inf = {"blocks_per_sm": 4}
+    one = cm.predict(cfg, shape, inf)
+    four = cm.predict(cfg + (4,), shape, inf)
+    assert four["blocks"] == 4 * one["blocks"] and four["pred_ms"] < one["pred_ms"]
+    # a shape that already fills the GPU gains nothing from splitting
+    big = (2048, 2048, 2048)
+    c = (128, 128, 4, 4, 32)
+    assert cm.predict(c + (2,), big, inf)["pred_ms"] > cm.predict(c, big, inf)["pred_ms"]
+    assert len(cm.default_config(2048, 2048, 2048)) == 5
+    assert cm.splits_of(cm.default_config(64, 4096, 4096)) > 1

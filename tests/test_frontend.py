@@ -163,6 +163,21 @@ def test_option_errors(opts, needle):
     assert needle in compile_err(tc.gen_mlir("mbr", 64, 64, 64), opts)
 
 
+def test_split_k_geometry_and_errors():
+    """split-k=S (a backend option) puts S workgroups per output tile on grid z."""
+    staged = "block-tile=64,64 thread-tile=4,4 tile-k=32 promote=1 vectorize=1"
+    l = _lib.Kernel(tc.gen_mlir("mbr", 64, 4096, 4096), staged + " split-k=8").launches()[0]
+    assert l["grid"] == [64, 1, 8] and l["block"] == [16, 16, 1]
+    assert _lib.Kernel(tc.gen_mlir("mbr", 64, 4096, 4096), staged).launches()[0]["grid"] == [64, 1, 1]
+    prog = tc.gen_mlir("mbr", 64, 64, 256)  # 8 slabs of 32
+    assert _lib.Kernel(prog, staged + " split-k=8").launches()[0]["grid"][2] == 8
+    assert compile_err(prog, staged + " split-k=9").endswith(
+        "error: tforge-gpu-pipeline: split-k 9 exceeds the 8 K slabs of this matmul")
+    assert compile_err(prog, "split-k=2").endswith("error: tforge-gpu-pipeline: split-k needs tile-k")
+    for bad in ("split-k=0", "split-k=65", "split-k=x"):
+        assert "invalid value" in compile_err(prog, staged + " " + bad)
+
+
 def test_options_accept_braces_bools_and_print_script(capfd):
     k = _lib.Kernel(tc.gen_mlir("mbr", 256, 256, 64),
                     "{block-tile=128,128 thread-tile=8,8 tile-k=32 promote=true vectorize=1 print-script=1}")

@@ -166,6 +166,47 @@ def test_resmlp_small():
     assert res["pass"], res
 
 
+@pytest.mark.parametrize("workload", ["mbr", "matmul"])
+@pytest.mark.parametrize("cfg,splits,shape", [
+    ((64, 64, 4, 4, 32), 8, (64, 4096, 4096)),     # the skinny measured shape
+    ((128, 128, 4, 4, 32), 3, (256, 256, 1024)),   # uneven slab ranges: 32 slabs over 3
+    ((64, 64, 4, 4, 16), 5, (128, 192, 80)),       # one slab per split
+    ((128, 64, 8, 4, 16), 2, (777, 1111, 333)),    # padded ragged problem
+])
+def test_split_k_bound(workload, cfg, splits, shape):
+    m, n, k = shape
+    opts = STAGED.format(*cfg) + f" split-k={splits}"
+    ins, out = run_prog(workload, m, n, k, opts, logical=cm.padded(cfg, m, n, k))
+    assert_bound(workload, ins, out)
+
+
+def test_split_k_handle_reuse_is_deterministic():
+    """The partial-sum workspace is reused across launches: after 30 launches
+    on one handle, a correctness run on it gives the bits of a fresh handle
+    (the slices are added in a fixed order)."""
+    m, n, k = 128, 512, 2048
+    opts = STAGED.format(64, 64, 4, 4, 32) + " split-k=7"
+    ins = o.make_inputs("mbr", m, n, k)
+    arrays = [np.ascontiguousarray(v) for v in ins.values()]
+    kern = _lib.Kernel(tc.gen_mlir("mbr", m, n, k), opts, "t.mlir")
+    first = np.empty((m, n), np.float32)
+    kern.run(arrays, first)
+    kern.bench(arrays, warmup=10, reps=20)
+    again = np.empty((m, n), np.float32)
+    kern.run(arrays, again)
+    _, fresh = run_prog("mbr", m, n, k, opts, ins=ins)
+    assert o.bitwise_diff(first, again) == 0 and o.bitwise_diff(first, fresh) == 0
+    assert_bound("mbr", ins, first)
+
+
+def test_split_k_resmlp():
+    m, n, k = 256, 128, 512
+    d, launch = tg.compile_kernel("resmlp", m, n, k, STAGED.format(128, 128, 4, 4, 32) + " split-k=4", tag="test")
+    assert [L["grid"][2] for L in launch["launches"]] == [4, 4]
+    res, out = tg.check("resmlp", m, n, k, d, launch)
+    assert res["pass"], res
+
+
 def test_info_and_bench_keys():
     d, launch = tg.compile_kernel("mbr", 1024, 1024, 1024, STAGED.format(128, 128, 8, 8, 32), tag="test")
     inf = tg.info("mbr", 1024, 1024, 1024, d, launch)

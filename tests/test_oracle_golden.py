@@ -115,6 +115,13 @@ def test_small_brute_force():
     assert o.bitwise_diff(o.epilogue(o.matmul_nofma(a, b), bias, relu=True), out) == 0
 
 
+def test_scalar_mnk_loop_is_the_nofma_form():
+    """The timed scalar baseline (default pipeline loop order) is bitwise the
+    no-FMA closed form that the E1 cpu-scalar rows pin, on a ragged shape."""
+    ins = o.make_inputs("matmul", 37, 53, 129)
+    assert o.bitwise_diff(o.matmul_scalar_mnk(ins["a"], ins["b"]), o.matmul_nofma(ins["a"], ins["b"])) == 0
+
+
 # ---- planted mistakes: each must break a pin -------------------------------
 
 def test_planted_wrong_order_fails_fma_pin():
