@@ -8,7 +8,8 @@ checked before timing:
   - reported: max |kernel - rocBLAS| on the same inputs
 Timing: 10 warm-up + 100 reps (HIP events), median; GPU clock sampled per rep
 through amdsmi; clock-adjusted metric = % of the FP32 matrix peak at the median
-clock (256 CUs x 256 FLOP/clk).  --cublas (alias --rocblas) also times rocBLAS
+clock (256 CUs x 256 FLOP/clk); element-op workloads (add, bias_add, relu)
+report GB/s of compulsory traffic and % of the 8 TB/s HBM peak.  --cublas (alias --rocblas) also times rocBLAS
 sgemm plus a separate epilogue kernel, the counterpart of the reference's
 cuBLAS row.
 
@@ -23,7 +24,10 @@ import sys
 import numpy as np
 
 from tensorforge_amd import provenance
+from tensorforge_amd import tforge_cpu as tc
 from tensorforge_amd import tforge_gpu as tg
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD's published figure
 
 SHAPES = [(256, 256, 256), (512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048),
           (4096, 4096, 4096), (1000, 1000, 1000), (777, 1111, 333)]
@@ -58,7 +62,8 @@ def main(argv=None):
 
     for workload in args.workloads.split(","):
         for m, n, k in shapes:
-            flops = 2.0 * m * n * k
+            unit, work = tc.flops_or_bytes(workload, m, n, k)
+            elementwise = unit == "GB/s"
             ref_blas = None
             if workload in ("matmul", "mbr"):
                 _, ref_blas = tg.check(workload, m, n, k, mode="rocblas")
@@ -82,10 +87,13 @@ def main(argv=None):
                 if out is None:
                     continue
                 r = tg.bench(workload, m, n, k, kdir, launch, mode, args.warmup, args.reps, args.flush)
-                gflops = flops / (r["median_ms"] * 1e-3) / 1e9
+                gflops = work / (r["median_ms"] * 1e-3) / 1e9  # GFLOP/s, or GB/s for element ops
                 clk = r["sm_clock_median_mhz"]
-                pct = 100.0 * gflops / tg.fp32_peak_gflops(clk) if clk > 0 else float("nan")
-                pct_nominal = 100.0 * gflops / tg.fp32_peak_gflops(tg.PEAK_CLOCK_MHZ)
+                if elementwise:
+                    pct = pct_nominal = 100.0 * gflops / HBM_PEAK_GBS
+                else:
+                    pct = 100.0 * gflops / tg.fp32_peak_gflops(clk) if clk > 0 else float("nan")
+                    pct_nominal = 100.0 * gflops / tg.fp32_peak_gflops(tg.PEAK_CLOCK_MHZ)
                 launch_str = f"grid={r['grid']} block={r['block']} padded={r['padded']}"
                 res = (f"regs={r['regs']} local={r['local_bytes']} smem={r['static_smem']} "
                        f"blocks/SM={r['blocks_per_sm']} occ={r['theo_occupancy']}")
@@ -97,16 +105,17 @@ def main(argv=None):
                 out.row(**base, device=r["gpu"], workload=workload, shape=shape_str(m, n, k),
                         dtype="f32", pipeline=pipeline, params=f"{name}; {launch_str}; {res}",
                         threads="", warmup=r["warmup"], reps=r["reps"], median_ms=r["median_ms"],
-                        min_ms=r["min_ms"], std_ms=r["std_ms"], metric="GFLOP/s",
+                        min_ms=r["min_ms"], std_ms=r["std_ms"], metric=unit,
                         metric_value=gflops, sm_clock_median_mhz=clk,
-                        clock_adjusted_metric=(f"{pct:.2f}% of FP32 matrix peak at median clock; "
+                        clock_adjusted_metric=(f"{pct:.2f}% of 8 TB/s HBM (compulsory bytes)" if elementwise else
+                                               f"{pct:.2f}% of FP32 matrix peak at median clock; "
                                                f"{pct_nominal:.2f}% of 157.3 TFLOP/s"),
                         alloc_bytes_per_call="",
                         correctness=f"err/bound={chk['err_over_bound']:.3g}; max|x-rocblas|={diff:.3g}",
                         notes=(f"l2_flush={r['l2_flush']}; gfx clock {r['sm_clock_min_mhz']}-"
                                f"{r['sm_clock_max_mhz']} MHz; power {r['power_median_w']} W; "
                                f"hip driver {r['hip_driver']}"))
-                print(f"        median {r['median_ms']:.4f} ms  {gflops:.1f} GFLOP/s  "
+                print(f"        median {r['median_ms']:.4f} ms  {gflops:.1f} {unit}  "
                       f"{pct_nominal:.1f}% of peak ({pct:.1f}% @ {clk:.0f} MHz)  {res}", flush=True)
     print(f"failures: {failures}")
     return 1 if failures else 0

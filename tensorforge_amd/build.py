@@ -74,11 +74,11 @@ def _demangle(names):
 
 
 def _entry_name(demangled):
-    m = re.search(r"staged_gemm_kernel<(\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+)>", demangled)
+    m = re.search(r"staged_gemm_kernel<(\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+)>", demangled)
     if m:
-        bm, bn, tm, tn, bk, p, v = m.groups()
+        bm, bn, tm, tn, bk, p, v, mk = m.groups()
         return (f"tf_staged_b{bm}x{bn}_t{tm}x{tn}_k{bk}" + ("" if p == "1" else "_noprom") +
-                ("" if v == "1" else "_novec"))
+                ("" if v == "1" else "_novec") + ("_masked" if mk == "1" else ""))
     m = re.search(r"(direct_gemm|elementwise)_kernel<(\d+), (\d+)>", demangled)
     if m:
         fam = "direct" if m.group(1) == "direct_gemm" else "elementwise"

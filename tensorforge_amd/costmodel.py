@@ -248,3 +248,15 @@ def default_config(m, n, k):
     """The cost model's pick for a shape, split-K factors included: what the
     backend uses when no autotuned configuration is recorded."""
     return rank(m, n, k, space=with_splits(config_space(), m, n, k))[0]
+
+
+def tuned_options(workload, m, n, k):
+    """Options for a shape: the autotuner's recorded best
+    (tuned_configs.json, written by bench/stage9_costmodel.py) if there is
+    one, else the cost model's pick."""
+    p = PKG / "tuned_configs.json"
+    if p.exists():
+        rec = json.loads(p.read_text()).get(f"{workload}/{m}x{n}x{k}")
+        if rec:
+            return rec["options"]
+    return options(default_config(m, n, k))

@@ -54,6 +54,24 @@ template <int TM, int TN>
 __global__ void elementwise_kernel(EltParams p) {
   const long m_base = ((long)blockIdx.y * blockDim.y + threadIdx.y) * TM;
   const long n_base = ((long)blockIdx.x * blockDim.x + threadIdx.x) * TN;
+  if constexpr (TN % 4 == 0) {
+    // Thread tiles 4k wide on aligned rows: 128-bit loads and stores, so a
+    // wave moves 64 x TN x 4 contiguous bytes per row.  Same IEEE ops.
+    if (p.vec_ok && n_base + TN <= p.N) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const long m = m_base + i;
+        if (m >= p.M) break;
+#pragma unroll
+        for (int j = 0; j < TN; j += 4) {
+          const int n = (int)n_base + j;
+          const f32x4 x = *reinterpret_cast<const f32x4 *>(p.X + m * p.ldx + n);
+          *reinterpret_cast<f32x4 *>(p.Y + m * p.ldy + n) = apply_epi4(x, p.epi, m, n);
+        }
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -80,13 +98,12 @@ hipError_t launch_elementwise(const EltParams &p, dim3 grid, dim3 block, hipStre
 // slice order, so the result does not depend on scheduling.
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(ReduceParams p) {
   const long q = (long)blockIdx.x * 256 + threadIdx.x;
-  const long per_row = p.N / 4;
+  const long per_row = (p.N + 3) / 4;
   if (q >= (long)p.M * per_row) return;
   const long m = q / per_row;
   const int n = (int)(q - m * per_row) * 4;
-  const long slice = (long)p.M * p.ldc;
-  const float *src = p.ws + m * p.ldc + n;
-  auto ld = [&](int s) { return *reinterpret_cast<const f32x4 *>(src + s * slice); };
+  const float *src = p.ws + m * p.ws_ld + n;
+  auto ld = [&](int s) { return *reinterpret_cast<const f32x4 *>(src + s * p.ws_slice); };
   f32x4 v = ld(0);
   int s = 1;
   for (; s + 4 <= p.splits; s += 4) {
@@ -97,11 +114,17 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(ReduceParams p) {
     v += t3;
   }
   for (; s < p.splits; ++s) v += ld(s);
-  *reinterpret_cast<f32x4 *>(p.C + m * p.ldc + n) = apply_epi4(v, p.epi, m, n);
+  if ((p.ldc & 3) == 0 && n + 4 <= p.N) {
+    *reinterpret_cast<f32x4 *>(p.C + m * p.ldc + n) = apply_epi4(v, p.epi, m, n);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (n + e < p.N) p.C[m * p.ldc + n + e] = apply_epi1(v[e], p.epi, m, n + e);
+  }
 }
 
 hipError_t launch_splitk_reduce(const ReduceParams &p, hipStream_t stream) {
-  const long quads = (long)p.M * (p.N / 4);
+  const long quads = (long)p.M * ((p.N + 3) / 4);
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
@@ -109,11 +132,11 @@ hipError_t launch_splitk_reduce(const ReduceParams &p, hipStream_t stream) {
 // The registry tables are host data (they hold host launch stubs).
 #ifndef __HIP_DEVICE_COMPILE__
 #define TF_DIRECT(TM, TN)                                                                       \
-  KernelEntry{FAM_DIRECT, 0, 0, TM, TN, 0, 0, 0, "tf_direct_t" #TM "x" #TN,                   \
+  KernelEntry{FAM_DIRECT, 0, 0, TM, TN, 0, 0, 0, 0, "tf_direct_t" #TM "x" #TN,                \
               reinterpret_cast<const void *>(&direct_gemm_kernel<TM, TN>), &launch_direct<TM, TN>, \
               nullptr, 0}
 #define TF_ELT(TM, TN)                                                                          \
-  KernelEntry{FAM_ELEMENTWISE, 0, 0, TM, TN, 0, 0, 0, "tf_elementwise_t" #TM "x" #TN,         \
+  KernelEntry{FAM_ELEMENTWISE, 0, 0, TM, TN, 0, 0, 0, 0, "tf_elementwise_t" #TM "x" #TN,      \
               reinterpret_cast<const void *>(&elementwise_kernel<TM, TN>), nullptr,             \
               &launch_elementwise<TM, TN>, 0}
 #define TF_BOTH(TM, TN) TF_DIRECT(TM, TN), TF_ELT(TM, TN)

@@ -34,7 +34,38 @@ __device__ __forceinline__ f32x4 apply_epi4(f32x4 v, const EpiParams &e, long m,
   return v;
 }
 
-// Scalar form for edge elements and the direct / elementwise kernels.
+// The same for C[m, n..n+3] at the right edge of a matrix whose rows are not
+// 16-byte aligned: operands are read element by element, columns >= N are
+// not read (their results are discarded).
+__device__ __forceinline__ f32x4 apply_epi4_edge(f32x4 v, const EpiParams &e, long m, int n, int N) {
+  auto ld4 = [&](const float *row) {
+    f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (n + c < N) t[c] = row[n + c];
+    return t;
+  };
+#pragma unroll
+  for (int i = 0; i < kMaxEpi; ++i) {
+    if (i >= e.nops) break;
+    const int kind = e.kind[i];
+    if (kind == EPI_BIAS) {
+      v += ld4(e.ptr[i]);
+    } else if (kind == EPI_RELU) {
+      v.x = relu_ieee(v.x);
+      v.y = relu_ieee(v.y);
+      v.z = relu_ieee(v.z);
+      v.w = relu_ieee(v.w);
+    } else if (kind == EPI_ADD) {
+      v += ld4(e.ptr[i] + m * e.ldr[i]);
+    } else if (kind == EPI_ADD_SELF) {
+      v = v + v;
+    }
+  }
+  return v;
+}
+
+// Scalar form for the direct / elementwise kernels.
 __device__ __forceinline__ float apply_epi1(float v, const EpiParams &e, long m, int n) {
 #pragma unroll
   for (int i = 0; i < kMaxEpi; ++i) {

@@ -566,6 +566,8 @@ bool parse_options(const std::string &text, Options &o, std::string &err) {
       if (!want_bool(o.print_script)) return false;
     } else if (key == "xcd-swizzle") {
       if (!want_bool(o.xcd_swizzle)) return false;
+    } else if (key == "mask-edges") {
+      if (!want_bool(o.mask_edges)) return false;
     } else if (key == "block-tile" || key == "thread-tile") {
       std::vector<int64_t> &dst = key == "block-tile" ? o.block_tile : o.thread_tile;
       if (!parse_list(val, dst)) {
@@ -691,7 +693,7 @@ bool plan_program(const Program &p, const Options &o, Plan &plan, std::string &e
       st.N = op.operand_types[1].shape[1];
       st.ops = "matmul";
       st.loc = op.loc;
-      if (o.tile_k > 0 && (st.M % o.bm || st.N % o.bn || st.K % o.tile_k)) {
+      if (o.tile_k > 0 && !o.mask_edges && (st.M % o.bm || st.N % o.bn || st.K % o.tile_k)) {
         err = format_error(p.source_name, op.loc,
                            "tforge-gpu-tile: tile-k needs static tiles; pad the problem to multiples of the block "
                            "and K tiles");

@@ -61,6 +61,7 @@ struct Options {
   bool print_script = false;
   bool xcd_swizzle = true;  // backend: XCD-aware tile order for staged kernels
   int64_t split_k = 1;      // backend: workgroups per output tile along K (staged kernels)
+  bool mask_edges = false;  // backend: staged kernels take any shape (masked edge tiles, no padding)
   // Derived (reference lib/Pipelines/Pipelines.cpp:214-263).
   int64_t bm = 16, bn = 16, tm = 1, tn = 1;
   bool align_vectors = false;

@@ -10,7 +10,8 @@ BM, BN in {32, 64, 128}, TM x TN in {4x4, 8x4, 4x8, 8x8}, BK in {8, 16, 32}),
 widened for CDNA4 (BM, BN up to 256, BK up to 64), restricted to the
 configurations that map onto whole waves of 32x32 MFMA blocks, plus the
 promote/vectorize ablation variants of the reference's Stage 8/9 ladders
-(bench/stage8_gpu.sh:7-14, bench/stage9_ablation.py:23-28).
+(bench/stage8_gpu.sh:7-14, bench/stage9_ablation.py:23-28), and a masked
+twin (any M, N, K; the mask-edges option) of every LDS-staged configuration.
 """
 
 import pathlib
@@ -57,12 +58,16 @@ def configs():
                                (128, 128, 8, 8, 16), (128, 128, 8, 8, 8)):
         for promote, vec in ((0, 1), (1, 0), (0, 0)):
             out.append((bm, bn, tm, tn, bk, promote, vec))
+    # Masked twins (mask-edges) of every LDS-staged configuration.
+    out = [c + (0,) for c in out]
+    out += [c[:7] + (1,) for c in out if c[5] == 1]
     return out
 
 
 def name(c):
-    bm, bn, tm, tn, bk, p, v = c
-    return f"tf_staged_b{bm}x{bn}_t{tm}x{tn}_k{bk}" + ("" if p else "_noprom") + ("" if v else "_novec")
+    bm, bn, tm, tn, bk, p, v, mk = c
+    return (f"tf_staged_b{bm}x{bn}_t{tm}x{tn}_k{bk}" + ("" if p else "_noprom") + ("" if v else "_novec")
+            + ("_masked" if mk else ""))
 
 
 def main(shards=16):
@@ -77,7 +82,8 @@ def main(shards=16):
             t = ", ".join(str(x) for x in c)
             lines.append(f"    KernelEntry{{FAM_STAGED, {t}, \"{name(c)}\",")
             lines.append(f"                reinterpret_cast<const void *>(&staged_gemm_kernel<{t}>),")
-            lines.append(f"                &launch_staged<{t}>, nullptr, StagedGemm<{t}>::LDS_BYTES}},")
+            t7 = ", ".join(str(x) for x in c[:7])
+            lines.append(f"                &launch_staged<{t}>, nullptr, StagedGemm<{t7}>::LDS_BYTES}},")
         lines += ["};", f"extern const int kStagedCount{i} = {len(part)};", "#else",
                   "// Device pass: instantiate the kernels the host table names."]
         for c in part:

@@ -95,10 +95,24 @@ int select_launches(tf_kernel *k) {
     Launch L;
     const bool gemm = st.kind == tff::STAGE_GEMM;
     const bool staged = gemm && o.tile_k > 0;
+    // Shapes that are not tile multiples (allowed by mask-edges) run the
+    // masked twin of the configuration.
+    const int masked = staged && (st.M % o.bm || st.N % o.bn || st.K % o.tile_k) ? 1 : 0;
+    if (masked && !o.promote)
+      return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc,
+                                                "tforge-gpu-pipeline: mask-edges needs promote=1 for shapes that are "
+                                                "not multiples of the block and K tiles"));
+    // Masked kernels index A and B with 32-bit offsets (tiles may run one
+    // block past the edges).
+    if (masked && ((st.M + 256) * st.K >= (1L << 31) || (st.K + 64) * (st.N + 256) >= (1L << 31)))
+      return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc,
+                                                "tforge-gpu-pipeline: mask-edges supports matrices below 2^31 "
+                                                "elements; pad this problem instead"));
     for (const tfk::KernelEntry *e = tfk::registry_begin(); e != tfk::registry_end(); ++e) {
       if (staged) {
         if (e->family == tfk::FAM_STAGED && e->bm == o.bm && e->bn == o.bn && e->tm == o.tm && e->tn == o.tn &&
-            e->bk == o.tile_k && e->promote == (int)o.promote && e->vectorize == (int)o.vectorize) {
+            e->bk == o.tile_k && e->promote == (int)o.promote && e->vectorize == (int)o.vectorize &&
+            e->masked == masked) {
           L.entry = e;
           break;
         }
@@ -127,13 +141,15 @@ int select_launches(tf_kernel *k) {
       if (!staged)
         return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc,
                                                   "tforge-gpu-pipeline: split-k needs tile-k"));
-      if (st.K / o.tile_k < o.split_k)
+      const long slabs = ceil_div(st.K, o.tile_k);
+      if (slabs < o.split_k)
         return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc,
                                                   "tforge-gpu-pipeline: split-k " + std::to_string(o.split_k) +
-                                                      " exceeds the " + std::to_string(st.K / o.tile_k) +
+                                                      " exceeds the " + std::to_string(slabs) +
                                                       " K slabs of this matmul"));
       L.grid.z = (unsigned)o.split_k;
-      k->ws_bytes = std::max(k->ws_bytes, (size_t)o.split_k * st.M * st.N * sizeof(float));
+      // Whole tiles per slice: (grid.y * BM) x (grid.x * BN).
+      k->ws_bytes = std::max(k->ws_bytes, (size_t)o.split_k * L.grid.y * o.bm * L.grid.x * o.bn * sizeof(float));
     }
     k->launches.push_back(L);
   }
@@ -180,7 +196,11 @@ int launch_stage(const tf_kernel *k, size_t s, void *const *ptrs, hipStream_t st
     p.epi = make_epi(st, ptrs);
     p.swizzle = k->opts.xcd_swizzle ? 1 : 0;
     p.splits = (int)L.grid.z;
-    if (p.splits > 1) p.ws = static_cast<float *>(k->ws);
+    if (p.splits > 1) {
+      p.ws = static_cast<float *>(k->ws);
+      p.ws_ld = (long)L.grid.x * L.entry->bn;
+      p.ws_slice = p.ws_ld * L.grid.y * L.entry->bm;
+    }
     err = L.entry->gemm(p, L.grid, L.block, stream);
     if (err == hipSuccess && p.splits > 1) {
       tfk::ReduceParams r{};
@@ -189,6 +209,8 @@ int launch_stage(const tf_kernel *k, size_t s, void *const *ptrs, hipStream_t st
       r.M = p.M;
       r.N = p.N;
       r.splits = p.splits;
+      r.ws_ld = p.ws_ld;
+      r.ws_slice = p.ws_slice;
       r.ldc = p.ldc;
       r.epi = p.epi;
       err = tfk::launch_splitk_reduce(r, stream);
@@ -202,6 +224,12 @@ int launch_stage(const tf_kernel *k, size_t s, void *const *ptrs, hipStream_t st
     p.ldx = st.N;
     p.ldy = st.N;
     p.epi = make_epi(st, ptrs);
+    bool vec = st.N % 4 == 0;
+    auto aligned = [](const void *q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+    vec = vec && aligned(p.X) && aligned(p.Y);
+    for (int i = 0; i < p.epi.nops; ++i)
+      if (p.epi.ptr[i]) vec = vec && aligned(p.epi.ptr[i]);
+    p.vec_ok = vec ? 1 : 0;
     err = L.entry->elt(p, L.grid, L.block, stream);
   }
   if (err != hipSuccess)

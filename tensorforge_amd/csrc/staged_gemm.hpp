@@ -34,8 +34,11 @@
 //    few output tiles (64 x 4096 x 4096) still fill 256 CUs.  Partial sums go
 //    to a workspace with ordinary cached stores; a second, HBM-bound kernel
 //    adds them in a fixed order (deterministic) and applies the epilogue.
-//  * Shapes must be multiples of (BM, BN, BK): the host pads, as the
-//    reference runner does (runners/gpu/tforge-gpu-bench.cu:214-232).
+//  * Shapes: multiples of (BM, BN, BK), padded by the host as the reference
+//    runner does (runners/gpu/tforge-gpu-bench.cu:214-232); or, with
+//    masked=1 (the mask-edges option), any shape: edge tiles and the K tail
+//    load zeros outside the matrices and store only inside, so the result is
+//    bit-identical to the padded problem's without the pad copies.
 #pragma once
 
 #include <type_traits>
@@ -65,6 +68,10 @@ __device__ __forceinline__ void staged_tile_coords(int gx, int gy, int swizzle, 
   tn = r / rows;
 }
 
+// Element e of a staging register (a float or a 4-vector).
+__device__ __forceinline__ float &elem(float &v, int) { return v; }
+__device__ __forceinline__ float &elem(f32x4 &v, int e) { return reinterpret_cast<float *>(&v)[e]; }
+
 template <int BM, int BN, int TM, int TN, int BK, int PROMOTE, int VEC>
 struct StagedGemm {
   static constexpr int NT = (BM / TM) * (BN / TN);
@@ -88,7 +95,7 @@ struct StagedGemm {
   static_assert(LDS_BYTES <= 160 * 1024, "LDS per workgroup exceeds 160 KB");
 };
 
-template <int BM, int BN, int TM, int TN, int BK, int PROMOTE, int VEC>
+template <int BM, int BN, int TM, int TN, int BK, int PROMOTE, int VEC, int MASK>
 __global__ void __launch_bounds__((BM / TM) * (BN / TN))
 staged_gemm_kernel(GemmParams p) {
   using G = StagedGemm<BM, BN, TM, TN, BK, PROMOTE, VEC>;
@@ -105,11 +112,17 @@ staged_gemm_kernel(GemmParams p) {
   const long m0 = (long)tile_m * BM, n0 = (long)tile_n * BN;
   const long lda = p.lda, ldb = p.ldb;
   // Split-K: workgroup z reduces K slabs [kb, ke).
+  const int nk_all = (p.K + BK - 1) / BK;
   const int splits = p.splits > 1 ? p.splits : 1, split = blockIdx.z;
-  const int kb = (int)((long)(p.K / BK) * split / splits);
-  const int ke = (int)((long)(p.K / BK) * (split + 1) / splits);
-  const float *__restrict__ A = p.A + m0 * lda + (long)kb * BK;
-  const float *__restrict__ B = p.B + n0 + (long)kb * BK * ldb;
+  const int kb = (int)((long)nk_all * split / splits);
+  const int ke = (int)((long)nk_all * (split + 1) / splits);
+  const long kbase = (long)kb * BK;
+  const float *__restrict__ A = p.A + m0 * lda + kbase;
+  const float *__restrict__ B = p.B + n0 + kbase * ldb;
+  // Masked shapes: tiles that cross M or N, slabs that cross K, and rows that
+  // are not 16-byte aligned take the guarded paths; the rest run unguarded.
+  static_assert(!MASK || PROMOTE, "masked instantiations stage through LDS");
+  const bool edge = MASK && (m0 + BM > p.M || n0 + BN > p.N);
 
   f32x16 acc[FM][FN];
 #pragma unroll
@@ -127,25 +140,103 @@ staged_gemm_kernel(GemmParams p) {
     using VT = typename std::conditional<VEC, f32x4, float>::type;
     VT ra[G::A_PER], rb[G::B_PER];
 
+    // Masked instantiations (MASK = 1).  Rows of A at or past M and columns of B at
+    // or past N only reach outputs that are never stored, so a slab that does
+    // not hold the last K row loads them from a nearby valid element (row
+    // M-1, column N-4) with the same 128-bit loads as the unmasked path.
+    // The slab holding row K-1 (and every slab when N < 4) is "guarded":
+    // element by element, with zeros outside the matrices, so the K tail adds
+    // exact zeros as the pad path's zero-padded copies do.  A and B rows that
+    // are not 16-byte aligned (K or N not a multiple of 4) use unaligned
+    // 128-bit loads, which gfx950 serves at 4-byte alignment.  Offsets are
+    // 32-bit from the matrices' base pointers (the host bounds M*K and K*N).
+    const int Mi = p.M, Ni = p.N, Ki = p.K, m0i = (int)m0, n0i = (int)n0, kbi = (int)kbase;
+    auto guarded = [&](int k0) { return MASK && (kbi + k0 + BK >= Ki || Ni < 4); };
+    auto a_in = [&](int q, int k0, int e) {
+      const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
+      return m0i + r < Mi && kbi + k0 + c + e < Ki;
+    };
+    auto b_in = [&](int q, int k0, int e) {
+      const int r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
+      return kbi + k0 + r < Ki && n0i + c + e < Ni;
+    };
+    auto load16 = [](const float *src) {
+      VT v;
+      __builtin_memcpy(&v, src, sizeof(VT));
+      return v;
+    };
     auto load_slab = [&](int k0) {
+      if constexpr (!MASK) {
 #pragma unroll
-      for (int it = 0; it < G::A_PER; ++it) {
-        const int q = tid + it * NT;
-        if (G::A_VECS % NT == 0 || q < G::A_VECS) {
-          const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
-          ra[it] = *reinterpret_cast<const VT *>(A + r * lda + k0 + c);
+        for (int it = 0; it < G::A_PER; ++it) {
+          const int q = tid + it * NT;
+          if (G::A_VECS % NT == 0 || q < G::A_VECS) {
+            const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
+            ra[it] = *reinterpret_cast<const VT *>(A + r * lda + k0 + c);
+          }
         }
-      }
 #pragma unroll
-      for (int it = 0; it < G::B_PER; ++it) {
-        const int q = tid + it * NT;
-        if (G::B_VECS % NT == 0 || q < G::B_VECS) {
-          const int r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
-          rb[it] = *reinterpret_cast<const VT *>(B + (k0 + r) * ldb + c);
+        for (int it = 0; it < G::B_PER; ++it) {
+          const int q = tid + it * NT;
+          if (G::B_VECS % NT == 0 || q < G::B_VECS) {
+            const int r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
+            rb[it] = *reinterpret_cast<const VT *>(B + (k0 + r) * ldb + c);
+          }
+        }
+      } else if (!guarded(k0)) {
+#pragma unroll
+        for (int it = 0; it < G::A_PER; ++it) {
+          const int q = tid + it * NT;
+          if (G::A_VECS % NT == 0 || q < G::A_VECS) {
+            const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
+            ra[it] = load16(p.A + (min(m0i + r, Mi - 1) * (int)lda + kbi + k0 + c));
+          }
+        }
+#pragma unroll
+        for (int it = 0; it < G::B_PER; ++it) {
+          const int q = tid + it * NT;
+          if (G::B_VECS % NT == 0 || q < G::B_VECS) {
+            const int r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
+            const int gn = n0i + c < Ni ? n0i + c : Ni - VW;
+            rb[it] = load16(p.B + ((kbi + k0 + r) * (int)ldb + gn));
+          }
+        }
+      } else {
+#pragma unroll
+        for (int it = 0; it < G::A_PER; ++it) {
+          const int q = tid + it * NT;
+          if (G::A_VECS % NT == 0 || q < G::A_VECS) {
+            const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
+            const int base = (m0i + r) * (int)lda + kbi + k0 + c;
+#pragma unroll
+            for (int e = 0; e < VW; ++e) elem(ra[it], e) = p.A[a_in(q, k0, e) ? base + e : 0];
+          }
+        }
+#pragma unroll
+        for (int it = 0; it < G::B_PER; ++it) {
+          const int q = tid + it * NT;
+          if (G::B_VECS % NT == 0 || q < G::B_VECS) {
+            const int r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
+            const int base = (kbi + k0 + r) * (int)ldb + n0i + c;
+#pragma unroll
+            for (int e = 0; e < VW; ++e) elem(rb[it], e) = p.B[b_in(q, k0, e) ? base + e : 0];
+          }
         }
       }
     };
-    auto store_slab = [&](int buf) {
+    auto store_slab = [&](int buf, int k0) {
+      if (MASK && guarded(k0)) {
+#pragma unroll
+        for (int it = 0; it < G::A_PER; ++it)
+#pragma unroll
+          for (int e = 0; e < VW; ++e)
+            if (!a_in(tid + it * NT, k0, e)) elem(ra[it], e) = 0.0f;
+#pragma unroll
+        for (int it = 0; it < G::B_PER; ++it)
+#pragma unroll
+          for (int e = 0; e < VW; ++e)
+            if (!b_in(tid + it * NT, k0, e)) elem(rb[it], e) = 0.0f;
+      }
 #pragma unroll
       for (int it = 0; it < G::A_PER; ++it) {
         const int q = tid + it * NT;
@@ -203,7 +294,7 @@ staged_gemm_kernel(GemmParams p) {
     };
     if (nk > 0) {
       load_slab(0);
-      store_slab(0);
+      store_slab(0, 0);
       if (nk > 1) load_slab(BK);
     }
     __syncthreads();
@@ -215,7 +306,7 @@ staged_gemm_kernel(GemmParams p) {
       for (int kc = 0; kc < C; ++kc) {
         const int fs = kc & 1;
         if (C == 1 && more) {
-          store_slab(cur ^ 1);
+          store_slab(cur ^ 1, (kt + 1) * BK);
           if (kt + 2 < nk) load_slab((kt + 2) * BK);
         }
         if (kc + 1 < C) {
@@ -236,7 +327,7 @@ staged_gemm_kernel(GemmParams p) {
               acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[fs][j][s], af[fs][i][s], acc[i][j], 0, 0, 0);
         if (C >= 2 && kc == MID && more) {
           __builtin_amdgcn_sched_barrier(0);
-          store_slab(cur ^ 1);
+          store_slab(cur ^ 1, (kt + 1) * BK);
           if (kt + 2 < nk) load_slab((kt + 2) * BK);
         }
       }
@@ -305,14 +396,41 @@ staged_gemm_kernel(GemmParams p) {
     // Split-K: this workgroup's partial sums go to slice `split` of the
     // workspace; splitk_reduce_kernel, launched next on the same stream, adds
     // the slices in order and runs the epilogue.
-    float *own = p.ws + split * (long)p.M * p.ldc;
+    // The workspace holds whole tiles (ws_ld is N rounded up to BN), so
+    // these stores need no masks.
+    float *own = p.ws + split * p.ws_slice;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j)
 #pragma unroll
         for (int g = 0; g < 4; ++g)
-          *reinterpret_cast<f32x4 *>(own + row_of(i) * p.ldc + col_of(j, g)) = group(i, j, g);
+          *reinterpret_cast<f32x4 *>(own + row_of(i) * p.ws_ld + col_of(j, g)) = group(i, j, g);
+    return;
+  }
+
+  if (MASK && (edge || (p.ldc & 3) != 0)) {
+    // Edge tile, or rows of C not 16-byte aligned: outputs outside C are
+    // dropped.  With N % 4 == 0 each group of 4 is wholly inside or outside.
+    const bool c_vec = (p.ldc & 3) == 0;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const long m = row_of(i);
+      if (m >= p.M) continue;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = col_of(j, g);
+          if (n >= p.N) continue;
+          if (c_vec) {
+            *reinterpret_cast<f32x4 *>(p.C + m * p.ldc + n) = apply_epi4(group(i, j, g), p.epi, m, n);
+          } else {
+            const f32x4 v = apply_epi4_edge(group(i, j, g), p.epi, m, n, p.N);
+            for (int e = 0; e < 4 && n + e < p.N; ++e) p.C[m * p.ldc + n + e] = v[e];
+          }
+        }
+    }
     return;
   }
 
@@ -339,9 +457,9 @@ staged_gemm_kernel(GemmParams p) {
   }
 }
 
-template <int BM, int BN, int TM, int TN, int BK, int PROMOTE, int VEC>
+template <int BM, int BN, int TM, int TN, int BK, int PROMOTE, int VEC, int MASK>
 hipError_t launch_staged(const GemmParams &p, dim3 grid, dim3 block, hipStream_t stream) {
-  hipLaunchKernelGGL((staged_gemm_kernel<BM, BN, TM, TN, BK, PROMOTE, VEC>), grid, block, 0, stream, p);
+  hipLaunchKernelGGL((staged_gemm_kernel<BM, BN, TM, TN, BK, PROMOTE, VEC, MASK>), grid, block, 0, stream, p);
   return hipGetLastError();
 }
 

@@ -42,14 +42,16 @@ struct GemmParams {
   // then forms C = epi(sum of the slices in order 0..splits-1).
   int splits;
   float *ws;
+  long ws_ld, ws_slice;  // partial-sum row stride and slice size (floats); whole tiles
 };
 
-// C[M x N] = epi(ws[0] + ws[1] + ... + ws[splits-1]), slices of M x ldc.
+// C[M x N] = epi(ws[0] + ws[1] + ... + ws[splits-1]); slice s starts at
+// ws + s * ws_slice, rows ws_ld apart (ws_ld a multiple of 4, >= N).
 struct ReduceParams {
   const float *ws;
   float *C;
   int M, N, splits;
-  long ldc;
+  long ws_ld, ws_slice, ldc;
   EpiParams epi;
 };
 
@@ -60,6 +62,7 @@ struct EltParams {
   int M, N;
   long ldx, ldy;
   EpiParams epi;
+  int vec_ok;  // 1: every operand 16-byte aligned with row strides a multiple of 4
 };
 
 enum Family : int { FAM_DIRECT = 0, FAM_STAGED = 1, FAM_ELEMENTWISE = 2 };
@@ -72,6 +75,7 @@ struct KernelEntry {
   int family;
   int bm, bn, tm, tn, bk;  // staged: full config; direct/elementwise: tm, tn only (bm = bn = bk = 0)
   int promote, vectorize;
+  int masked;  // staged: 1 = any M, N, K (edges masked in-kernel); 0 = tile multiples only
   const char *name;
   const void *fn;  // the __global__ function, for hipFuncGetAttributes / occupancy
   GemmLauncher gemm;
@@ -79,8 +83,7 @@ struct KernelEntry {
   int lds_bytes;   // static LDS of the instantiation
 };
 
-// The split-K reduction (direct_kernels.hip); N and ldc multiples of 4,
-// ws and C 16-byte aligned.
+// The split-K reduction (direct_kernels.hip); ws and C 16-byte aligned.
 hipError_t launch_splitk_reduce(const ReduceParams &p, hipStream_t stream);
 
 // Registry (defined in the generated registry translation unit).

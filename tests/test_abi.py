@@ -81,6 +81,10 @@ def test_registry_covers_config_space_and_resources():
     assert set(cm.config_space()) <= staged
     ablation = {e["cfg"] for e in reg if e["family"] == "staged" and e["cfg"][5:] != (1, 1)}
     assert (128, 64, 8, 4, 16, 0, 1) in ablation and (128, 64, 8, 4, 16, 1, 0) in ablation
+    # every LDS-staged configuration has a masked twin (mask-edges)
+    plain = {e["cfg"] for e in reg if e["family"] == "staged" and not e["name"].endswith("_masked")}
+    masked = {e["cfg"] for e in reg if e["family"] == "staged" and e["name"].endswith("_masked")}
+    assert masked == {c for c in plain if c[5] == 1}
     res = json.loads((_lib.PKG / "kernel_resources.json").read_text())
     for e in reg:
         assert e["name"] in res, e["name"]

@@ -16,6 +16,7 @@ import pytest
 
 from tensorforge_amd import _lib
 from tensorforge_amd import tforge_cpu as tc
+from tensorforge_amd import tforge_gpu as tg
 
 GOLDEN = pathlib.Path(__file__).resolve().parent / "golden"
 
@@ -176,6 +177,22 @@ def test_split_k_geometry_and_errors():
     assert compile_err(prog, "split-k=2").endswith("error: tforge-gpu-pipeline: split-k needs tile-k")
     for bad in ("split-k=0", "split-k=65", "split-k=x"):
         assert "invalid value" in compile_err(prog, staged + " " + bad)
+
+
+def test_mask_edges_accepts_any_shape():
+    """mask-edges=1 (a backend option) lifts the NOTPADDED rule: the grid
+    covers the shape with ceil-divided tiles and the kernel masks edges."""
+    staged = "block-tile=128,64 thread-tile=8,4 tile-k=16 promote=1 vectorize=1"
+    prog = tc.gen_mlir("mbr", 777, 1111, 333)
+    assert "tile-k needs static tiles" in compile_err(prog, staged)
+    l = _lib.Kernel(prog, staged + " mask-edges=1").launches()[0]
+    assert l["grid"] == [18, 7, 1] and (l["m"], l["n"], l["k"]) == (777, 1111, 333)
+    assert _lib.Kernel(prog, staged + " mask-edges=1 split-k=3").launches()[0]["grid"] == [18, 7, 3]
+    assert "mask-edges needs promote=1" in compile_err(prog, staged.replace("promote=1", "promote=0") + " mask-edges")
+    # multiples of the tiles need no masks, so promote=0 is fine there
+    _lib.Kernel(tc.gen_mlir("mbr", 256, 128, 64), staged.replace("promote=1", "promote=0") + " mask-edges=1")
+    assert tg.padded_shape(777, 1111, 333, staged + " mask-edges=1") == (777, 1111, 333)
+    assert tg.padded_shape(777, 1111, 333, "{" + staged + " mask-edges}") == (777, 1111, 333)
 
 
 def test_options_accept_braces_bools_and_print_script(capfd):

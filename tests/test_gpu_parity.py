@@ -81,7 +81,8 @@ def test_staged_padded_ragged(workload):
 
 def test_every_staged_instantiation():
     """Each ahead-of-time instantiation (all promote / vectorize variants) on
-    a small problem padded to its tiles."""
+    a small problem padded to its tiles; each masked twin on a problem that
+    is ragged in M, N and K."""
     ins_cache = {}
     failures = []
     for e in _lib.registry():
@@ -89,12 +90,17 @@ def test_every_staged_instantiation():
             continue
         bm, bn, tm, tn, bk, p, v = e["cfg"]
         m, n, k = 2 * bm, 2 * bn, 2 * bk if bk >= 32 else 64
+        masked = e["name"].endswith("_masked")
+        if masked:
+            m, n, k = m - 3, n - 5, k - 7
         key = (m, n, k)
         if key not in ins_cache:
             ins = o.make_inputs("mbr", m, n, k)
             ins_cache[key] = (ins,) + o.fp64_reference("mbr", ins)
         ins, ref, bound = ins_cache[key]
         opts = f"block-tile={bm},{bn} thread-tile={tm},{tn} tile-k={bk} promote={p} vectorize={v}"
+        if masked:
+            opts += " mask-edges=1"
         print(f"instantiation {e['name']} at {m}x{n}x{k}", flush=True)
         _, out = run_prog("mbr", m, n, k, opts, ins=ins)
         eob = o.e1_metrics(out, ref, bound)["max_err_over_bound"]
@@ -112,10 +118,15 @@ def test_headline_2048(opts):
     assert res["err_over_bound"] < 0.05
 
 
-@pytest.mark.parametrize("workload,shape", [("relu", (999, 1001)), ("bias_add", (33, 17)), ("add", (1024, 1024))])
-def test_elementwise_bit_exact(workload, shape):
+@pytest.mark.parametrize("workload,shape", [("relu", (999, 1001)), ("bias_add", (33, 17)), ("add", (1024, 1024)),
+                                            ("bias_add", (300, 1024)), ("relu", (64, 36))])
+@pytest.mark.parametrize("opts", ["block-tile=16,16 thread-tile=1,1", "block-tile=4,256 thread-tile=1,4",
+                                  "block-tile=8,512 thread-tile=2,8"])
+def test_elementwise_bit_exact(workload, shape, opts):
+    """Scalar and 128-bit paths (thread tiles 4k wide on aligned rows; ragged
+    and unaligned widths fall back per element) are bit-exact."""
     m, n = shape
-    d, launch = tg.compile_kernel(workload, m, n, None, "block-tile=16,16 thread-tile=1,1", tag="test")
+    d, launch = tg.compile_kernel(workload, m, n, None, opts, tag="test")
     res, out = tg.check(workload, m, n, None, d, launch)
     assert res["pass"], res
 
@@ -205,6 +216,42 @@ def test_split_k_resmlp():
     assert [L["grid"][2] for L in launch["launches"]] == [4, 4]
     res, out = tg.check("resmlp", m, n, k, d, launch)
     assert res["pass"], res
+
+
+MASKED_SHAPES = [(777, 1111, 333), (1000, 1000, 1000), (67, 17, 33), (1, 1, 1), (130, 258, 1031), (64, 4095, 4097)]
+
+
+@pytest.mark.parametrize("workload", ["mbr", "matmul"])
+@pytest.mark.parametrize("shape", MASKED_SHAPES)
+@pytest.mark.parametrize("cfg,extra", [((128, 64, 8, 4, 16), ""), ((128, 128, 4, 4, 32), ""),
+                                       ((64, 64, 4, 4, 32), " split-k=3"),
+                                       ((64, 64, 4, 4, 32), " vectorize=0")])
+def test_masked_edges_equal_pad_path_bits(workload, shape, cfg, extra):
+    """mask-edges=1 on the true shape gives the bits of the reference's pad
+    path (zero-padded copies, padded kernel, unpad): the same tiles see the
+    same zeros.  Both pass the FP64 bound."""
+    m, n, k = shape
+    opts = STAGED.format(*cfg) + extra
+    if "vectorize=0" in extra:
+        opts = opts.replace("vectorize=1 vectorize=0", "vectorize=0")
+    if "split-k" in extra and cm.padded(cfg, m, n, k)[2] // cfg[4] < 3:
+        pytest.skip("fewer K slabs than splits")
+    ins = o.make_inputs(workload, m, n, k)
+    _, masked = run_prog(workload, m, n, k, opts + " mask-edges=1", ins=ins)
+    _, padded = run_prog(workload, m, n, k, opts, ins=ins, logical=cm.padded(cfg, m, n, k))
+    assert o.bitwise_diff(masked, padded) == 0
+    assert_bound(workload, ins, masked)
+
+
+def test_masked_resmlp_ragged():
+    """Residual block at a shape that is not a multiple of the tiles."""
+    m, n, k = 200, 72, 136
+    ins = tc.make_inputs("resmlp", m, n, k)
+    opts = STAGED.format(64, 64, 4, 4, 32) + " mask-edges=1"
+    kern = _lib.Kernel(tc.gen_mlir("resmlp", m, n, k), opts, "t.mlir")
+    y = np.empty((m, n), np.float32)
+    kern.run([np.ascontiguousarray(v) for v in ins.values()], y)
+    assert tg._resmlp_check(ins, y)["pass"]
 
 
 def test_info_and_bench_keys():
