@@ -115,7 +115,10 @@ int tf_device_info(tf_device_info_t *out);
  * parse `options` (--tforge-gpu-pipeline option string, may be empty), plan the
  * launches and select the gfx950 instantiations.  No GPU work: runs on a host
  * without a GPU.  Replaces python/tforge_gpu.py:66-91 (compile_kernel's
- * tool chain). */
+ * tool chain).  Options are the reference's (include/TensorForge/Pipelines.h:45-72)
+ * plus three backend options: split-k=S (S workgroups per output tile along K,
+ * then an ordered reduction launch), mask-edges (staged kernels accept shapes
+ * that are not tile multiples) and xcd-swizzle (default on). */
 int tf_compile(const char *source_name, const char *program, const char *options, tf_kernel_t **out);
 void tf_kernel_free(tf_kernel_t *k);
 
@@ -127,9 +130,11 @@ int tf_kernel_info(const tf_kernel_t *k, int launch, tf_kernel_resources_t *out)
 
 /* Kernel ABI: enqueue every launch of the program on `stream` (a hipStream_t,
  * NULL for the default stream) with caller-owned device buffers in argN order,
- * shaped as compiled.  Intermediates of multi-launch programs are allocated
- * once per handle on first use.  No synchronisation.  Replaces cuLaunchKernel
- * with the marshalled argN list (runners/gpu/tforge-gpu-bench.cu:259-299). */
+ * shaped as compiled.  Intermediates of multi-launch programs and the split-K
+ * partial-sum workspace are allocated once per handle on first use; calls on
+ * one handle that overlap on different streams share them.  No
+ * synchronisation.  Replaces cuLaunchKernel with the marshalled argN list
+ * (runners/gpu/tforge-gpu-bench.cu:259-299). */
 int tf_launch(tf_kernel_t *k, void *const *device_buffers, void *stream);
 
 /* Correctness run, as the runner's "--warmup 0 --reps 1 --in-dir --out":

@@ -58,15 +58,23 @@ __global__ void elementwise_kernel(EltParams p) {
     // Thread tiles 4k wide on aligned rows: 128-bit loads and stores, so a
     // wave moves 64 x TN x 4 contiguous bytes per row.  Same IEEE ops.
     if (p.vec_ok && n_base + TN <= p.N) {
+      // All loads first (rows past M read row M-1 and are not stored), so
+      // they are in flight together; then the ops and the stores.
+      f32x4 x[TM][TN / 4];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const long m = min(m_base + i, (long)p.M - 1);
+#pragma unroll
+        for (int j = 0; j < TN / 4; ++j) x[i][j] = *reinterpret_cast<const f32x4 *>(p.X + m * p.ldx + n_base + 4 * j);
+      }
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const long m = m_base + i;
         if (m >= p.M) break;
 #pragma unroll
-        for (int j = 0; j < TN; j += 4) {
-          const int n = (int)n_base + j;
-          const f32x4 x = *reinterpret_cast<const f32x4 *>(p.X + m * p.ldx + n);
-          *reinterpret_cast<f32x4 *>(p.Y + m * p.ldy + n) = apply_epi4(x, p.epi, m, n);
+        for (int j = 0; j < TN / 4; ++j) {
+          const int n = (int)n_base + 4 * j;
+          *reinterpret_cast<f32x4 *>(p.Y + m * p.ldy + n) = apply_epi4(x[i][j], p.epi, m, n);
         }
       }
       return;

@@ -726,6 +726,12 @@ bool plan_program(const Program &p, const Options &o, Plan &plan, std::string &e
     Stage &st = plan.stages[open];
     EpiOp e{tfk::EPI_NONE, -1};
     if (op.name == "relu") {
+      // relu(relu(x)) == relu(x) bit for bit (lib/Dialect/TForge/TForgeFolders.cpp,
+      // ReluOp::fold: relu's results are NaN or >= +0.0, fixed points of maximum(., +0.0)).
+      if (!st.epi.empty() && st.epi.back().kind == tfk::EPI_RELU) {
+        open_value = op.result;
+        continue;
+      }
       e.kind = tfk::EPI_RELU;
     } else if (op.name == "bias_add") {
       e.kind = tfk::EPI_BIAS;

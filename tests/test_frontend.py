@@ -164,6 +164,20 @@ def test_option_errors(opts, needle):
     assert needle in compile_err(tc.gen_mlir("mbr", 64, 64, 64), opts)
 
 
+def test_relu_of_relu_folds_into_one_epilogue_op():
+    """ReluOp::fold (lib/Dialect/TForge/TForgeFolders.cpp): relu is idempotent,
+    so a fused relu after relu adds no operation."""
+    t = "tensor<64x64xf32>"
+    prog = (f"func.func @entry(%a: {t}, %b: {t}) -> {t} {{\n"
+            f"  %0 = tforge.matmul %a, %b : {t}, {t} -> {t}\n"
+            f"  %1 = tforge.relu %0 : {t} -> {t}\n"
+            f"  %2 = tforge.relu %1 : {t} -> {t}\n"
+            f"  %3 = tforge.relu %2 : {t} -> {t}\n"
+            f"  return %3 : {t}\n}}\n")
+    (l,) = _lib.Kernel(prog).launches()
+    assert l["ops"] == "matmul+relu"
+
+
 def test_split_k_geometry_and_errors():
     """split-k=S (a backend option) puts S workgroups per output tile on grid z."""
     staged = "block-tile=64,64 thread-tile=4,4 tile-k=32 promote=1 vectorize=1"
