@@ -66,6 +66,8 @@ def main(argv=None):
                     help="split-K factors to cross with the configuration grid, e.g. 1,2,4,8 (backend option)")
     ap.add_argument("--tuned", default=str(TUNED), help="JSON table the best configuration is recorded in")
     ap.add_argument("--no-record", action="store_true", help="do not record the best configuration")
+    ap.add_argument("--prewarm", type=int, default=500,
+                    help="untimed launches of the first configuration per shape before timing (GPU clock settles)")
     args = ap.parse_args(argv)
     shapes = SHAPES
     if args.shapes:
@@ -125,6 +127,9 @@ def main(argv=None):
         t2 = time.time()
         meas = {}
         got = np.empty((m, n), np.float32)
+        if args.prewarm and compiled:
+            c0, d0, l0 = compiled[0]
+            tg.bench(wl, m, n, k, d0, l0, warmup=args.prewarm, reps=1)
         for c, d, l in compiled:
             kern = _lib.Kernel((d / "input.mlir").read_text(), l["options"], str(d / "input.mlir"))
             logical = None if tuple(l["padded"]) == (m, n, k) else (m, n, k)
