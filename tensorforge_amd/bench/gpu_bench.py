@@ -16,6 +16,9 @@ cuBLAS row.
   python -m tensorforge_amd.bench.gpu_bench --csv results/gpu/stage8.csv --tag stage8 \\
       --variant full-128x128-t8x8-k32="block-tile=128,128 thread-tile=8,8 tile-k=32 promote=1 vectorize=1" \\
       --cublas
+
+A variant's options may be @tuned (per shape: the autotuned options, else the cost model's pick) or
+@tuned-masked (the same, with mask-edges where the shape is not a tile multiple).
 """
 
 import argparse
@@ -23,6 +26,7 @@ import sys
 
 import numpy as np
 
+from tensorforge_amd import costmodel as cm
 from tensorforge_amd import provenance
 from tensorforge_amd import tforge_cpu as tc
 from tensorforge_amd import tforge_gpu as tg
@@ -67,7 +71,16 @@ def main(argv=None):
             ref_blas = None
             if workload in ("matmul", "mbr"):
                 _, ref_blas = tg.check(workload, m, n, k, mode="rocblas")
-            rows = [(name, opts, "kernel") for name, opts in variants]
+            rows = []
+            for name, opts in variants:
+                # @tuned: the autotuned (else cost-model) options of this shape; @tuned-masked: the same
+                # with mask-edges on shapes that are not tile multiples.
+                if opts in ("@tuned", "@tuned-masked") and workload in ("matmul", "mbr"):
+                    t = cm.tuned_options(workload, m, n, k)
+                    if opts == "@tuned-masked" and tg.padded_shape(m, n, k, t) != (m, n, k):
+                        t += " mask-edges=1"
+                    opts = t
+                rows.append((name, opts, "kernel"))
             if args.blas and workload in ("matmul", "mbr"):
                 rows.append(("rocblas", "", "rocblas"))
             for name, opts, mode in rows:
