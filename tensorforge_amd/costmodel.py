@@ -84,9 +84,20 @@ def _valid_staged(bm, bn, tm, tn, bk):
     if threads % 64 or threads > 1024 or threads * tm * tn > 32768:
         return False
     wtm, wtn = 8 * tm, 8 * tn
-    if wtm % 32 or wtn % 32 or bm % wtm or bn % wtn or bk % 8:
+    if wtm % 16 or wtn % 16 or bm % wtm or bn % wtn:
         return False
-    return 2 * (bm * (bk + 4) + bk * (bn + 8)) * 4 <= 160 * 1024
+    if bk % (256 // _block(tm, tn)):
+        return False
+    return _lds_bytes(bm, bn, tm, tn, bk) <= 160 * 1024
+
+
+def _block(tm, tn):
+    """MFMA block edge: 32 when the wave tile (8*TM x 8*TN) is made of 32x32 blocks, else 16."""
+    return 32 if (8 * tm) % 32 == 0 and (8 * tn) % 32 == 0 else 16
+
+
+def _lds_bytes(bm, bn, tm, tn, bk):
+    return 2 * (bm * (bk + 4) + bk * (bn + (8 if _block(tm, tn) == 32 else 4))) * 4
 
 
 def reference_space():
@@ -105,13 +116,21 @@ def reference_space():
 
 def config_space():
     """The CDNA4 grid: BM, BN in {32..256}, TM x TN in {4x4, 8x4, 4x8, 8x8},
-    BK in {8..64}, every configuration that has a gfx950 instantiation (whole
-    waves of 32x32 MFMA blocks, LDS within 160 KiB)."""
+    BK in {8..64} (32x32 MFMA blocks), and BM, BN in {32..128}, TM x TN in
+    {2x2, 2x4, 4x2}, BK in {16..64} (16x16 blocks): every configuration that
+    has a gfx950 instantiation (whole waves of MFMA blocks, LDS within 160 KiB,
+    the register file)."""
     out = []
     for bm in (32, 64, 128, 256):
         for bn in (32, 64, 128, 256):
             for tm, tn in ((4, 4), (8, 4), (4, 8), (8, 8)):
                 for bk in (8, 16, 32, 64):
+                    if _valid_staged(bm, bn, tm, tn, bk):
+                        out.append((bm, bn, tm, tn, bk))
+    for bm in (32, 64, 128):
+        for bn in (32, 64, 128):
+            for tm, tn in ((2, 2), (2, 4), (4, 2)):
+                for bk in (16, 32, 64):
                     if _valid_staged(bm, bn, tm, tn, bk):
                         out.append((bm, bn, tm, tn, bk))
     return out
@@ -168,7 +187,7 @@ def estimate_info(cfg, target=MI355X, resources=None):
     occ = rec.get("occupancy_waves_per_simd", target.max_waves_per_simd)
     if occ is None or occ <= 0:
         occ = target.max_waves_per_simd
-    lds = rec.get("lds_bytes", 2 * (bm * (bk + 4) + bk * (bn + 8)) * 4)
+    lds = rec.get("lds_bytes", _lds_bytes(bm, bn, tm, tn, bk))
     by_regs = (occ * target.simds) // w
     by_lds = target.lds_per_cu // lds if lds else by_regs
     return {"blocks_per_sm": max(1, min(by_regs, by_lds, 2048 // threads)), "threads": threads}
@@ -201,10 +220,14 @@ def predict(cfg, padded, info, clock_mhz=None, target=MI355X):
                 "bound": "dram" if t_dram > t_compute else ("smem" if lds_step > fma_step else "fma"),
                 "latency_exposed": exposed > 0, "intensity": 2.0 * bm * bn / (4.0 * (bm + bn))}
     w = threads // 64
-    fm, fn = tm // 4, tn // 4
+    mb = _block(tm, tn)
+    fm, fn = 8 * tm // mb, 8 * tn // mb
     q = math.ceil(resident * w / target.simds)
-    mfma_step = q * fm * fn * (bk / 2) * target.mfma_cycles
-    lds_bytes = resident * (w * (bk / 8) * 1024 * (fm + fn) + (bm + bn) * bk * 4)
+    # FP32 MFMA: 64 FLOP per SIMD clock for both block sizes (4096 FLOP in 64
+    # cycles, or 2048 in 32); a wave's slab is 2 * (8 TM)(8 TN) BK FLOP.
+    mfma_step = q * 2 * (8 * tm) * (8 * tn) * bk / 64.0 * (target.mfma_cycles / 64.0)
+    # per chunk of 256 / mb k values, 1 KiB per A block-row and per B block-column
+    lds_bytes = resident * (w * (bk / (256 // mb)) * 1024 * (fm + fn) + (bm + bn) * bk * 4)
     lds_step = lds_bytes / target.lds_bytes_per_cycle
     l2_step = resident * (bm + bn) * bk * 4 / target.l2_bytes_per_cycle
     compute = max(mfma_step, lds_step, l2_step)

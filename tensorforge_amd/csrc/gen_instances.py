@@ -8,7 +8,8 @@ which tf_compile searches at run time.
 The configuration space is the reference's Stage 9 grid (python/costmodel.py:49-60:
 BM, BN in {32, 64, 128}, TM x TN in {4x4, 8x4, 4x8, 8x8}, BK in {8, 16, 32}),
 widened for CDNA4 (BM, BN up to 256, BK up to 64), restricted to the
-configurations that map onto whole waves of 32x32 MFMA blocks, plus the
+configurations that map onto whole waves of 32x32 MFMA blocks, thread tiles
+2x2 / 2x4 / 4x2 on 16x16 MFMA blocks for small block tiles, plus the
 promote/vectorize ablation variants of the reference's Stage 8/9 ladders
 (bench/stage8_gpu.sh:7-14, bench/stage9_ablation.py:23-28), and a masked
 twin (any M, N, K; the mask-edges option) of every LDS-staged configuration.
@@ -34,13 +35,14 @@ def staged_valid(bm, bn, tm, tn, bk, promote=1):
         return (f"{threads} threads x {tm * tn} accumulators per lane exceed the register file "
                 "(512 VGPRs per SIMD lane shared by the block's waves)")
     wtm, wtn = 8 * tm, 8 * tn
-    if wtm % 32 or wtn % 32:
-        return f"wave tile {wtm}x{wtn} (8*TM x 8*TN) is not made of 32x32 MFMA blocks"
+    if wtm % 16 or wtn % 16:
+        return f"wave tile {wtm}x{wtn} (8*TM x 8*TN) is not made of 16x16 or 32x32 MFMA blocks"
     if bm % wtm or bn % wtn:
         return f"block tile {bm}x{bn} is not a multiple of the wave tile {wtm}x{wtn} (8*TM x 8*TN)"
-    if bk % 8:
-        return "tile-k must be a multiple of 8"
-    lds = 2 * (bm * (bk + 4) + bk * (bn + 8)) * 4 if promote else 0
+    mb = 32 if wtm % 32 == 0 and wtn % 32 == 0 else 16
+    if bk % (256 // mb):
+        return f"tile-k must be a multiple of {256 // mb} for {mb}x{mb} MFMA blocks"
+    lds = 2 * (bm * (bk + 4) + bk * (bn + (8 if mb == 32 else 4))) * 4 if promote else 0
     if lds > LDS_LIMIT:
         return f"LDS {lds} B exceeds 160 KiB"
     return None
@@ -52,6 +54,13 @@ def configs():
         for bn in (32, 64, 128, 256):
             for tm, tn in ((4, 4), (8, 4), (4, 8), (8, 8)):
                 for bk in (8, 16, 32, 64):
+                    if staged_valid(bm, bn, tm, tn, bk) is None:
+                        out.append((bm, bn, tm, tn, bk, 1, 1))
+    # 16x16 MFMA blocks: small block tiles with 4x the waves.
+    for bm in (32, 64, 128):
+        for bn in (32, 64, 128):
+            for tm, tn in ((2, 2), (2, 4), (4, 2)):
+                for bk in (16, 32, 64):
                     if staged_valid(bm, bn, tm, tn, bk) is None:
                         out.append((bm, bn, tm, tn, bk, 1, 1))
     for bm, bn, tm, tn, bk in ((128, 64, 8, 4, 16), (64, 64, 4, 4, 16), (64, 64, 4, 4, 32),

@@ -46,14 +46,17 @@ std::string staged_reason(long bm, long bn, long tm, long tn, long bk, bool prom
     return std::to_string(threads) + " threads x " + std::to_string(tm * tn) +
            " accumulators per lane exceed the register file (512 VGPRs per SIMD lane shared by the block's waves)";
   const long wtm = 8 * tm, wtn = 8 * tn;
-  if (wtm % 32 || wtn % 32)
+  if (wtm % 16 || wtn % 16)
     return "wave tile " + std::to_string(wtm) + "x" + std::to_string(wtn) +
-           " (8*TM x 8*TN) is not made of 32x32 MFMA blocks";
+           " (8*TM x 8*TN) is not made of 16x16 or 32x32 MFMA blocks";
   if (bm % wtm || bn % wtn)
     return "block tile " + std::to_string(bm) + "x" + std::to_string(bn) + " is not a multiple of the wave tile " +
            std::to_string(wtm) + "x" + std::to_string(wtn) + " (8*TM x 8*TN)";
-  if (bk % 8) return "tile-k must be a multiple of 8";
-  const long lds = promote ? 2 * (bm * (bk + 4) + bk * (bn + 8)) * 4 : 0;
+  const long mb = (wtm % 32 == 0 && wtn % 32 == 0) ? 32 : 16, kc = 256 / mb;
+  if (bk % kc)
+    return "tile-k must be a multiple of " + std::to_string(kc) + " for " + std::to_string(mb) + "x" +
+           std::to_string(mb) + " MFMA blocks";
+  const long lds = promote ? 2 * (bm * (bk + 4) + bk * (bn + (mb == 32 ? 8 : 4))) * 4 : 0;
   if (lds > 160 * 1024) return "LDS " + std::to_string(lds) + " B exceeds 160 KiB";
   return "no ahead-of-time instantiation of this configuration in libtforge_hip";
 }

@@ -6,17 +6,20 @@
 //  * Option mapping.  block-tile=BM,BN is the workgroup tile; the workgroup has
 //    (BM/TM)*(BN/TN) threads as in the reference, i.e. that many / 64 waves.
 //    thread-tile=TM,TN gives each lane TM*TN accumulators, so a wave owns an
-//    (8*TM) x (8*TN) output tile built from 32x32 MFMA blocks.
-//  * Math.  v_mfma_f32_32x32x2_f32 with the operands swapped (the B tile feeds
-//    src0, the A tile src1), so each lane's accumulators are 4 consecutive
-//    columns of one output row: the epilogue reads bias with one 128-bit load
-//    and writes C with 128-bit stores.
-//  * K order.  Within a k-chunk of 8, lane half h and MFMA step s take
-//    k = 8*kc + 4*h + s, so every lane's A fragment is 4 consecutive k of one
-//    row (one ds_read_b128) and its B fragment 4 rows of one column.  The sum
-//    order differs from the reference's sequential k; parity is the
-//    reference's own FP64 error bound, which holds for any order
-//    (python/tforge_cpu.py:263-271).
+//    (8*TM) x (8*TN) output tile built from MB x MB MFMA blocks: MB = 32 when
+//    both sides are multiples of 32 (v_mfma_f32_32x32x2_f32), else MB = 16
+//    (v_mfma_f32_16x16x4_f32, the same FP32 rate), which lets small block
+//    tiles (thread-tile 2,2 / 2,4 / 4,2) run 4x as many waves.
+//  * Math.  The MFMA with the operands swapped (the B tile feeds src0, the A
+//    tile src1), so each lane's accumulators are runs of 4 consecutive columns
+//    of one output row: the epilogue reads bias with one 128-bit load and
+//    writes C with 128-bit stores.
+//  * K order.  A k-chunk holds KC = 256 / MB k values; lane group g = lane / MB
+//    and MFMA step s take k = KC*kc + 4*g + s, so every lane's A fragment is 4
+//    consecutive k of one row (one ds_read_b128) and its B fragment 4 rows of
+//    one column.  The sum order differs from the reference's sequential k;
+//    parity is the reference's own FP64 error bound, which holds for any
+//    order (python/tforge_cpu.py:263-271).
 //  * Staging (promote=1).  A tile [BM][BK+4] and B tile [BK][BN+8] in LDS,
 //    double-buffered, one barrier per slab.  Global loads run 1.5 slabs
 //    ahead, the next slab is written to LDS in the middle of the current one
@@ -50,6 +53,16 @@ namespace tfk {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// One MFMA on an MB x MB block: acc += src0 (4 x MB, from B) ^T-contracted with
+// src1 (from A); see the lane layouts in the header comment.
+template <int MB>
+using AccOf = typename std::conditional<MB == 32, f32x16, f32x4>::type;
+template <int MB>
+__device__ __forceinline__ AccOf<MB> mfma_block(float b, float a, AccOf<MB> c) {
+  if constexpr (MB == 32) return __builtin_amdgcn_mfma_f32_32x32x2f32(b, a, c, 0, 0, 0);
+  else return __builtin_amdgcn_mfma_f32_16x16x4f32(b, a, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ void staged_tile_coords(int gx, int gy, int swizzle, int &tm, int &tn) {
   int w = blockIdx.y * gx + blockIdx.x;
   const int total = gx * gy;
@@ -78,9 +91,13 @@ struct StagedGemm {
   static constexpr int NT = (BM / TM) * (BN / TN);
   static constexpr int WTM = 8 * TM, WTN = 8 * TN;
   static constexpr int NWM = BM / WTM, NWN = BN / WTN;
-  static constexpr int FM = WTM / 32, FN = WTN / 32;
+  static constexpr int MB = (WTM % 32 == 0 && WTN % 32 == 0) ? 32 : 16;  // MFMA block
+  static constexpr int KC = 256 / MB;                                     // k per chunk
+  static constexpr int FM = WTM / MB, FN = WTN / MB;
   static constexpr int LDA = BK + 4;  // LDS A row stride (floats): odd multiple of 4
-  static constexpr int LDB = BN + 8;  // LDS B row stride (floats)
+  // LDS B row stride: the 64 / MB lane groups read rows 4 apart; +8 (MB = 32)
+  // or +4 (MB = 16) puts them in disjoint banks.
+  static constexpr int LDB = BN + (MB == 32 ? 8 : 4);
   static constexpr int A_ELEMS = BM * LDA, B_ELEMS = BK * LDB;
   static constexpr int LDS_BYTES = PROMOTE ? 2 * (A_ELEMS + B_ELEMS) * 4 : 0;
   // Global -> register staging per thread and slab.
@@ -90,8 +107,8 @@ struct StagedGemm {
 
   static_assert(BM % TM == 0 && BN % TN == 0, "block tile must be a multiple of the thread tile");
   static_assert(NWM * NWN * 64 == NT, "waves must tile the block");
-  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be made of 32x32 MFMA blocks");
-  static_assert(BK % 8 == 0, "tile-k must be a multiple of 8");
+  static_assert(WTM % 16 == 0 && WTN % 16 == 0, "wave tile must be made of 16x16 or 32x32 MFMA blocks");
+  static_assert(BK % KC == 0, "tile-k must be a multiple of the k-chunk (8 for 32x32 blocks, 16 for 16x16)");
   static_assert(NT <= 1024, "at most 1024 threads per workgroup");
   static_assert(LDS_BYTES <= 160 * 1024, "LDS per workgroup exceeds 160 KB");
 };
@@ -101,12 +118,13 @@ __global__ void __launch_bounds__((BM / TM) * (BN / TN))
 staged_gemm_kernel(GemmParams p) {
   using G = StagedGemm<BM, BN, TM, TN, BK, PROMOTE, VEC>;
   constexpr int NT = G::NT, WTM = G::WTM, WTN = G::WTN, NWN = G::NWN, FM = G::FM, FN = G::FN;
-  constexpr int LDA = G::LDA, LDB = G::LDB, VW = G::VW;
+  constexpr int LDA = G::LDA, LDB = G::LDB, VW = G::VW, MB = G::MB, KC = G::KC;
+  using AccT = AccOf<MB>;
 
   const int tid = threadIdx.y * blockDim.x + threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / NWN, wn = wave - wm * NWN;
-  const int l32 = lane & 31, h = lane >> 5;
+  const int lr = lane % MB, lg = lane / MB;  // row/column within a block, k group
 
   int tile_m, tile_n;
   staged_tile_coords(gridDim.x, gridDim.y, p.swizzle, tile_m, tile_n);
@@ -125,13 +143,13 @@ staged_gemm_kernel(GemmParams p) {
   static_assert(!MASK || PROMOTE, "masked instantiations stage through LDS");
   const bool edge = MASK && (m0 + BM > p.M || n0 + BN > p.N);
 
-  f32x16 acc[FM][FN];
+  AccT acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+      for (int r = 0; r < MB * MB / 64; ++r) acc[i][j][r] = 0.0f;
 
   const int nk = ke - kb;
 
@@ -256,7 +274,7 @@ staged_gemm_kernel(GemmParams p) {
       }
     };
 
-    // Schedule per slab t (slab t lives in buffer t & 1, C = BK / 8 chunks):
+    // Schedule per slab t (slab t lives in buffer t & 1, C = BK / KC chunks):
     //   chunk kc:     read chunk kc+1's fragments, then chunk kc's MFMAs
     //   chunk C/2-1:  after its MFMAs, store slab t+1 (registers, loaded one
     //                 slab earlier) into the other buffer and issue the global
@@ -270,15 +288,15 @@ staged_gemm_kernel(GemmParams p) {
     // which precedes every read of it.
     // MID < C - 1 whenever C >= 2, so slab t+1's stores always precede the
     // barrier at chunk C-1; with a single chunk they are issued before it.
-    constexpr int C = BK / 8, MID = C >= 2 ? C / 2 - 1 : 0;
+    constexpr int C = BK / KC, MID = C >= 2 ? C / 2 - 1 : 0;
     f32x4 af[2][FM];
     float bf[2][FN][4];
     auto load_frags = [&](int buf, int kc, int slot) {
-      const float *as = As[buf] + (wm * WTM + l32) * LDA + 4 * h + kc * 8;
-      const float *bs = Bs[buf] + (4 * h + kc * 8) * LDB + wn * WTN + l32;
+      const float *as = As[buf] + (wm * WTM + lr) * LDA + 4 * lg + kc * KC;
+      const float *bs = Bs[buf] + (4 * lg + kc * KC) * LDB + wn * WTN + lr;
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
-        const float *src = as + i * 32 * LDA;
+        const float *src = as + i * MB * LDA;
         if constexpr (VEC) {
           af[slot][i] = *reinterpret_cast<const f32x4 *>(src);
         } else {
@@ -291,7 +309,7 @@ staged_gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int j = 0; j < FN; ++j)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) bf[slot][j][s] = bs[s * LDB + j * 32];
+        for (int s = 0; s < 4; ++s) bf[slot][j][s] = bs[s * LDB + j * MB];
     };
     if (nk > 0) {
       load_slab(0);
@@ -322,7 +340,7 @@ staged_gemm_kernel(GemmParams p) {
           for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[fs][j][s], af[fs][i][s], acc[i][j], 0, 0, 0);
+              acc[i][j] = mfma_block<MB>(bf[fs][j][s], af[fs][i][s], acc[i][j]);
         // Interleave the next chunk's LDS reads with this chunk's MFMAs, so a
         // wave issues its reads while its (dependent) MFMAs occupy the matrix
         // pipe instead of before them (measured at 2048^3: 143.8 -> 134.5 us
@@ -361,17 +379,17 @@ staged_gemm_kernel(GemmParams p) {
     }
   } else {
     // promote=0: fragments straight from global memory, no LDS, no barriers.
-    const float *ag = A + (long)(wm * WTM + l32) * lda + 4 * h;
-    const float *bg = B + 4 * h * ldb + wn * WTN + l32;
+    const float *ag = A + (long)(wm * WTM + lr) * lda + 4 * lg;
+    const float *bg = B + 4 * lg * ldb + wn * WTN + lr;
     for (int kt = 0; kt < nk; ++kt) {
       const int k0 = kt * BK;
 #pragma unroll
-      for (int kc = 0; kc < BK / 8; ++kc) {
+      for (int kc = 0; kc < BK / KC; ++kc) {
         f32x4 af[FM];
         float bf[FN][4];
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
-          const float *src = ag + (long)i * 32 * lda + k0 + kc * 8;
+          const float *src = ag + (long)i * MB * lda + k0 + kc * KC;
           if constexpr (VEC) {
             af[i] = *reinterpret_cast<const f32x4 *>(src);
           } else {
@@ -384,20 +402,22 @@ staged_gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
-          for (int s = 0; s < 4; ++s) bf[j][s] = bg[(long)(k0 + kc * 8 + s) * ldb + j * 32];
+          for (int s = 0; s < 4; ++s) bf[j][s] = bg[(long)(k0 + kc * KC + s) * ldb + j * MB];
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
           for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[j][s], af[i][s], acc[i][j], 0, 0, 0);
+              acc[i][j] = mfma_block<MB>(bf[j][s], af[i][s], acc[i][j]);
       }
     }
   }
 
-  // Epilogue: lane (l32, h) holds, per 32x32 block and group g, C[m, n..n+3]
-  // with m = row l32 of the block and n = 8*g + 4*h.
+  // Epilogue: lane (lr, lg) holds, per block and group g < NG, C[m, n..n+3]
+  // with m = row lr of the block and n = 8*g + 4*lg (MB = 32, 4 groups) or
+  // n = 4*lg (MB = 16, one group).
+  constexpr int NG = MB == 32 ? 4 : 1;
   auto group = [&](int i, int j, int g) {
     f32x4 v;
     v.x = acc[i][j][4 * g + 0];
@@ -406,8 +426,8 @@ staged_gemm_kernel(GemmParams p) {
     v.w = acc[i][j][4 * g + 3];
     return v;
   };
-  auto row_of = [&](int i) { return m0 + wm * WTM + i * 32 + l32; };
-  auto col_of = [&](int j, int g) { return (int)n0 + wn * WTN + j * 32 + 8 * g + 4 * h; };
+  auto row_of = [&](int i) { return m0 + wm * WTM + i * MB + lr; };
+  auto col_of = [&](int j, int g) { return (int)n0 + wn * WTN + j * MB + 8 * g + 4 * lg; };
 
   if (splits > 1) {
     // Split-K: this workgroup's partial sums go to slice `split` of the
@@ -421,7 +441,7 @@ staged_gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int j = 0; j < FN; ++j)
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
+        for (int g = 0; g < NG; ++g)
           *reinterpret_cast<f32x4 *>(own + row_of(i) * p.ws_ld + col_of(j, g)) = group(i, j, g);
     return;
   }
@@ -437,7 +457,7 @@ staged_gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int j = 0; j < FN; ++j)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
+        for (int g = 0; g < NG; ++g) {
           const int n = col_of(j, g);
           if (n >= p.N) continue;
           if (c_vec) {
@@ -458,7 +478,7 @@ staged_gemm_kernel(GemmParams p) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
+      for (int g = 0; g < NG; ++g) {
         const int n = col_of(j, g);
         f32x4 v = apply_epi4(group(i, j, g), p.epi, m, n);
         if constexpr (VEC) {

@@ -43,8 +43,11 @@ def test_cdna4_space_is_whole_mfma_waves():
     for bm, bn, tm, tn, bk in space:
         threads = (bm // tm) * (bn // tn)
         assert threads % 64 == 0 and threads <= 1024
-        assert bm % (8 * tm) == 0 and bn % (8 * tn) == 0 and bk % 8 == 0
-        assert 2 * (bm * (bk + 4) + bk * (bn + 8)) * 4 <= 160 * 1024
+        assert bm % (8 * tm) == 0 and bn % (8 * tn) == 0
+        mb = 32 if (8 * tm) % 32 == 0 and (8 * tn) % 32 == 0 else 16
+        assert (8 * tm) % mb == 0 and (8 * tn) % mb == 0 and bk % (256 // mb) == 0
+        assert 2 * (bm * (bk + 4) + bk * (bn + (8 if mb == 32 else 4))) * 4 <= 160 * 1024
+    assert (64, 64, 2, 2, 16) in space  # 16x16 blocks: 16 waves on a 64x64 tile
 
 
 @pytest.mark.parametrize("shape", [(2048, 2048, 2048), (8192, 1024, 4096), (64, 4096, 4096), (4096, 4096, 256)])
