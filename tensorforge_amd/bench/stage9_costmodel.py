@@ -44,10 +44,10 @@ def spearman(x, y):
     return float(np.corrcoef(rx, ry)[0, 1])
 
 
-def record_tuned(path, workload, m, n, k, cfg, ms, extra):
+def record_tuned(path, workload, m, n, k, cfg, ms, extra, suffix=""):
     path = pathlib.Path(path)
     table = json.loads(path.read_text()) if path.exists() else {}
-    table[f"{workload}/{m}x{n}x{k}"] = {"options": cm.options(cfg), "config": cm.name(cfg), "median_ms": ms,
+    table[f"{workload}/{m}x{n}x{k}"] = {"options": cm.options(cfg) + suffix, "config": cm.name(cfg), "median_ms": ms,
                                          "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12, **extra}
     path.write_text(json.dumps(table, indent=1, sort_keys=True) + "\n")
 
@@ -66,6 +66,8 @@ def main(argv=None):
                     help="split-K factors to cross with the configuration grid, e.g. 1,2,4,8 (backend option)")
     ap.add_argument("--tuned", default=str(TUNED), help="JSON table the best configuration is recorded in")
     ap.add_argument("--no-record", action="store_true", help="do not record the best configuration")
+    ap.add_argument("--mask-edges", action="store_true",
+                    help="run every configuration on the true shape with mask-edges (no pad copies)")
     ap.add_argument("--prewarm", type=int, default=500,
                     help="untimed launches of the first configuration per shape before timing (GPU clock settles)")
     args = ap.parse_args(argv)
@@ -87,6 +89,7 @@ def main(argv=None):
     base_space = cm.config_space() if args.space == "cdna4" else cm.reference_space()
     split_factors = tuple(int(v) for v in args.split_k.split(","))
     wl = args.workload
+    suffix = " mask-edges=1" if args.mask_edges else ""
     for m, n, k in shapes:
         space = cm.with_splits(base_space, m, n, k, split_factors)
         tag = f"stage9/{m}x{n}x{k}"
@@ -94,7 +97,7 @@ def main(argv=None):
         compiled, failed = [], []
         for cfg in space:
             try:
-                d, launch = tg.compile_kernel(wl, m, n, k, cm.options(cfg), tag=f"{tag}/{cm.name(cfg)}")
+                d, launch = tg.compile_kernel(wl, m, n, k, cm.options(cfg) + suffix, tag=f"{tag}/{cm.name(cfg)}")
                 compiled.append((cfg, d, launch))
             except RuntimeError as e:  # recorded, config excluded
                 failed.append((cfg, str(e).splitlines()[0][:200]))
@@ -106,7 +109,7 @@ def main(argv=None):
         preds = {}
         for c, d, l in compiled:
             inf = tg.info(wl, m, n, k, d, l)
-            preds[c] = (cm.predict(c, l["padded"], inf), inf)
+            preds[c] = (cm.predict(c, cm.padded(c, m, n, k), inf), inf)  # a masked kernel runs the padded tiles
         t_model = time.time() - t1
         pick = min(preds, key=lambda c: preds[c][0]["pred_ms"])
         if args.top:
@@ -146,7 +149,7 @@ def main(argv=None):
             meas[c] = (r, gf, pct, eob)
             p, inf = preds[c]
             out.row(**base, device=r["gpu"], workload=wl, shape=f"{m}x{n}x{k}", dtype="f32",
-                    pipeline=f"tforge-gpu-pipeline{{{cm.options(c)}}}",
+                    pipeline=f"tforge-gpu-pipeline{{{cm.options(c) + suffix}}}",
                     params=(f"{cm.name(c)}; grid={r['grid']} block={r['block']} padded={r['padded']}; "
                             f"regs={inf['regs']} smem={inf['static_smem']} blocks/SM={inf['blocks_per_sm']} "
                             f"occ={inf['theo_occupancy']}"),
@@ -181,7 +184,7 @@ def main(argv=None):
         if not args.no_record:
             record_tuned(args.tuned, wl, m, n, k, best, rb["median_ms"],
                          {"model_pick": cm.name(pick), "model_pick_ms": rp["median_ms"],
-                          "speedup_over_model_pick": rp["median_ms"] / rb["median_ms"], "spearman": rho})
+                          "speedup_over_model_pick": rp["median_ms"] / rb["median_ms"], "spearman": rho}, suffix)
         print(f"{m}x{n}x{k}: model {cm.name(pick)} {rp['median_ms']:.4f} ms ({pp:.1f}%), "
               f"best {cm.name(best)} {rb['median_ms']:.4f} ms ({pb:.1f}%), ratio raw "
               f"{rb['median_ms'] / rp['median_ms']:.3f} clock-adj {pp / pb:.3f}, spearman {rho:.3f}, "
