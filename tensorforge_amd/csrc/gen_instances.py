@@ -67,10 +67,22 @@ def configs():
                                (128, 128, 8, 8, 16), (128, 128, 8, 8, 8)):
         for promote, vec in ((0, 1), (1, 0), (0, 0)):
             out.append((bm, bn, tm, tn, bk, promote, vec))
-    # Masked twins (mask-edges) of every LDS-staged configuration.
+    # Masked twins (mask-edges) of the LDS-staged configurations whose threads
+    # stage at most MASK_MAX_VECTORS vectors per slab (more does not fit the
+    # register file next to the masked loads).
     out = [c + (0,) for c in out]
-    out += [c[:7] + (1,) for c in out if c[5] == 1]
+    out += [c[:7] + (1,) for c in out if c[5] == 1 and staging_vectors(*c[:5], c[6]) <= MASK_MAX_VECTORS]
     return out
+
+
+MASK_MAX_VECTORS = 16
+
+
+def staging_vectors(bm, bn, tm, tn, bk, vec=1):
+    """Global-load vectors (128-bit, or 32-bit without vectorize) a thread stages per slab."""
+    threads = (bm // tm) * (bn // tn)
+    vw = 4 if vec else 1
+    return -(-(bm * bk // vw) // threads) + -(-(bk * bn // vw) // threads)
 
 
 def name(c):

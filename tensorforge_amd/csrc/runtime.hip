@@ -127,6 +127,17 @@ int select_launches(tf_kernel *k) {
         }
       }
     }
+    if (!L.entry && masked) {
+      const long threads = (o.bm / o.tm) * (o.bn / o.tn);
+      const long vw = o.vectorize ? 4 : 1;
+      const long vecs = (o.bm * o.tile_k / vw + threads - 1) / threads + (o.tile_k * o.bn / vw + threads - 1) / threads;
+      if (vecs > 16)
+        return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc,
+                                                  "tforge-gpu-pipeline: mask-edges has no instantiation for a "
+                                                  "configuration whose threads stage " + std::to_string(vecs) +
+                                                      " vectors per slab (at most 16); use more threads or a smaller "
+                                                      "tile-k, or pad the problem"));
+    }
     if (!L.entry) {
       std::string why = staged ? staged_reason(o.bm, o.bn, o.tm, o.tn, o.tile_k, o.promote)
                                : "thread-tile " + std::to_string(o.tm) + "," + std::to_string(o.tn) +

@@ -21,12 +21,17 @@
 //    parity is the reference's own FP64 error bound, which holds for any
 //    order (python/tforge_cpu.py:263-271).
 //  * Staging (promote=1).  A tile [BM][BK+4] and B tile [BK][BN+8] in LDS,
-//    double-buffered, one barrier per slab.  Global loads run 1.5 slabs
-//    ahead, the next slab is written to LDS in the middle of the current one
-//    (overlapping MFMAs), and the barrier sits before the slab's last chunk so
-//    those MFMAs hide the next slab's first LDS reads.  Each chunk's MFMAs
-//    are interleaved with the next chunk's fragment reads.  Row padding makes
-//    the b128 fragment reads and the b32 B reads bank-conflict-free.
+//    double-buffered, one barrier per slab.  Two register staging sets where
+//    a thread stages few vectors: the global loads of slab t+3 are issued in
+//    the middle of slab t, two slabs before they are written to LDS (in the
+//    middle of slab t+2), so the LDS writes do not wait on HBM latency under
+//    full-chip load (one set, 1.5 slabs ahead, for the register-heavy
+//    configurations); the slab loop is unrolled by two so buffer and set
+//    indices are compile-time.  The barrier
+//    sits before the slab's last chunk so those MFMAs hide the next slab's
+//    first LDS reads.  Each chunk's MFMAs are interleaved with the next
+//    chunk's fragment reads.  Row padding makes the b128 fragment reads and
+//    the b32 B reads bank-conflict-free.
 //  * vectorize=1: 128-bit global loads and LDS accesses; vectorize=0: 32-bit.
 //  * promote=0: no LDS; each wave streams its fragments from global memory
 //    (through L2), the reference's "+tiling" rung (bench/stage9_ablation.py:23-28).
@@ -82,9 +87,9 @@ __device__ __forceinline__ void staged_tile_coords(int gx, int gy, int swizzle, 
   tn = r / rows;
 }
 
-// Element e of a staging register (a float or a 4-vector).
-__device__ __forceinline__ float &elem(float &v, int) { return v; }
-__device__ __forceinline__ float &elem(f32x4 &v, int e) { return reinterpret_cast<float *>(&v)[e]; }
+// Write element e of a staging register (a float or a 4-vector).
+__device__ __forceinline__ void put(float &v, int, float x) { v = x; }
+__device__ __forceinline__ void put(f32x4 &v, int e, float x) { v[e] = x; }
 
 template <int BM, int BN, int TM, int TN, int BK, int PROMOTE, int VEC>
 struct StagedGemm {
@@ -157,7 +162,10 @@ staged_gemm_kernel(GemmParams p) {
     __shared__ __attribute__((aligned(16))) float As[2][G::A_ELEMS];
     __shared__ __attribute__((aligned(16))) float Bs[2][G::B_ELEMS];
     using VT = typename std::conditional<VEC, f32x4, float>::type;
-    VT ra[G::A_PER], rb[G::B_PER];
+    // Staging sets in registers: two (loads two slabs ahead) when a thread
+    // stages few vectors per slab, else one (loads 1.5 slabs ahead).
+    constexpr int DEPTH = (G::A_PER + G::B_PER) <= (MASK ? 4 : 8) ? 2 : 1;
+    VT ra[DEPTH][G::A_PER], rb[DEPTH][G::B_PER];
 
     // Masked instantiations (MASK = 1).  Rows of A at or past M and columns of B at
     // or past N only reach outputs that are never stored, so a slab that does
@@ -170,12 +178,12 @@ staged_gemm_kernel(GemmParams p) {
     // 128-bit loads, which gfx950 serves at 4-byte alignment.  Offsets are
     // 32-bit from the matrices' base pointers (the host bounds M*K and K*N).
     const int Mi = p.M, Ni = p.N, Ki = p.K, m0i = (int)m0, n0i = (int)n0, kbi = (int)kbase;
-    auto guarded = [&](int k0) { return MASK && (kbi + k0 + BK >= Ki || Ni < 4); };
-    auto a_in = [&](int q, int k0, int e) {
+    auto guarded = [&](int k0) __attribute__((always_inline)) { return MASK && (kbi + k0 + BK >= Ki || Ni < 4); };
+    auto a_in = [&](int q, int k0, int e) __attribute__((always_inline)) {
       const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
       return m0i + r < Mi && kbi + k0 + c + e < Ki;
     };
-    auto b_in = [&](int q, int k0, int e) {
+    auto b_in = [&](int q, int k0, int e) __attribute__((always_inline)) {
       const int r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
       return kbi + k0 + r < Ki && n0i + c + e < Ni;
     };
@@ -184,14 +192,17 @@ staged_gemm_kernel(GemmParams p) {
       __builtin_memcpy(&v, src, sizeof(VT));
       return v;
     };
-    auto load_slab = [&](int k0) {
+    // `sc` is std::integral_constant<int, set>: the staging set is compile-time
+    // even where the lambda is not inlined, so the registers stay registers.
+    auto load_slab = [&](auto sc, int k0) __attribute__((always_inline)) {
+      constexpr int set = decltype(sc)::value;
       if constexpr (!MASK) {
 #pragma unroll
         for (int it = 0; it < G::A_PER; ++it) {
           const int q = tid + it * NT;
           if (G::A_VECS % NT == 0 || q < G::A_VECS) {
             const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
-            ra[it] = *reinterpret_cast<const VT *>(A + r * lda + k0 + c);
+            ra[set][it] = *reinterpret_cast<const VT *>(A + r * lda + k0 + c);
           }
         }
 #pragma unroll
@@ -199,7 +210,7 @@ staged_gemm_kernel(GemmParams p) {
           const int q = tid + it * NT;
           if (G::B_VECS % NT == 0 || q < G::B_VECS) {
             const int r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
-            rb[it] = *reinterpret_cast<const VT *>(B + (k0 + r) * ldb + c);
+            rb[set][it] = *reinterpret_cast<const VT *>(B + (k0 + r) * ldb + c);
           }
         }
       } else if (!guarded(k0)) {
@@ -208,7 +219,7 @@ staged_gemm_kernel(GemmParams p) {
           const int q = tid + it * NT;
           if (G::A_VECS % NT == 0 || q < G::A_VECS) {
             const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
-            ra[it] = load16(p.A + (min(m0i + r, Mi - 1) * (int)lda + kbi + k0 + c));
+            ra[set][it] = load16(p.A + (min(m0i + r, Mi - 1) * (int)lda + kbi + k0 + c));
           }
         }
 #pragma unroll
@@ -217,7 +228,7 @@ staged_gemm_kernel(GemmParams p) {
           if (G::B_VECS % NT == 0 || q < G::B_VECS) {
             const int r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
             const int gn = n0i + c < Ni ? n0i + c : Ni - VW;
-            rb[it] = load16(p.B + ((kbi + k0 + r) * (int)ldb + gn));
+            rb[set][it] = load16(p.B + ((kbi + k0 + r) * (int)ldb + gn));
           }
         }
       } else {
@@ -228,7 +239,7 @@ staged_gemm_kernel(GemmParams p) {
             const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
             const int base = (m0i + r) * (int)lda + kbi + k0 + c;
 #pragma unroll
-            for (int e = 0; e < VW; ++e) elem(ra[it], e) = p.A[a_in(q, k0, e) ? base + e : 0];
+            for (int e = 0; e < VW; ++e) put(ra[set][it], e, p.A[a_in(q, k0, e) ? base + e : 0]);
           }
         }
 #pragma unroll
@@ -238,30 +249,31 @@ staged_gemm_kernel(GemmParams p) {
             const int r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
             const int base = (kbi + k0 + r) * (int)ldb + n0i + c;
 #pragma unroll
-            for (int e = 0; e < VW; ++e) elem(rb[it], e) = p.B[b_in(q, k0, e) ? base + e : 0];
+            for (int e = 0; e < VW; ++e) put(rb[set][it], e, p.B[b_in(q, k0, e) ? base + e : 0]);
           }
         }
       }
     };
-    auto store_slab = [&](int buf, int k0) {
+    auto store_slab = [&](auto sc, int buf, int k0) __attribute__((always_inline)) {
+      constexpr int set = decltype(sc)::value;
       if (MASK && guarded(k0)) {
 #pragma unroll
         for (int it = 0; it < G::A_PER; ++it)
 #pragma unroll
           for (int e = 0; e < VW; ++e)
-            if (!a_in(tid + it * NT, k0, e)) elem(ra[it], e) = 0.0f;
+            if (!a_in(tid + it * NT, k0, e)) put(ra[set][it], e, 0.0f);
 #pragma unroll
         for (int it = 0; it < G::B_PER; ++it)
 #pragma unroll
           for (int e = 0; e < VW; ++e)
-            if (!b_in(tid + it * NT, k0, e)) elem(rb[it], e) = 0.0f;
+            if (!b_in(tid + it * NT, k0, e)) put(rb[set][it], e, 0.0f);
       }
 #pragma unroll
       for (int it = 0; it < G::A_PER; ++it) {
         const int q = tid + it * NT;
         if (G::A_VECS % NT == 0 || q < G::A_VECS) {
           const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
-          *reinterpret_cast<VT *>(&As[buf][r * LDA + c]) = ra[it];
+          *reinterpret_cast<VT *>(&As[buf][r * LDA + c]) = ra[set][it];
         }
       }
 #pragma unroll
@@ -269,7 +281,7 @@ staged_gemm_kernel(GemmParams p) {
         const int q = tid + it * NT;
         if (G::B_VECS % NT == 0 || q < G::B_VECS) {
           const int r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
-          *reinterpret_cast<VT *>(&Bs[buf][r * LDB + c]) = rb[it];
+          *reinterpret_cast<VT *>(&Bs[buf][r * LDB + c]) = rb[set][it];
         }
       }
     };
@@ -291,7 +303,7 @@ staged_gemm_kernel(GemmParams p) {
     constexpr int C = BK / KC, MID = C >= 2 ? C / 2 - 1 : 0;
     f32x4 af[2][FM];
     float bf[2][FN][4];
-    auto load_frags = [&](int buf, int kc, int slot) {
+    auto load_frags = [&](int buf, int kc, int slot) __attribute__((always_inline)) {
       const float *as = As[buf] + (wm * WTM + lr) * LDA + 4 * lg + kc * KC;
       const float *bs = Bs[buf] + (4 * lg + kc * KC) * LDB + wn * WTN + lr;
 #pragma unroll
@@ -312,21 +324,26 @@ staged_gemm_kernel(GemmParams p) {
         for (int s = 0; s < 4; ++s) bf[slot][j][s] = bs[s * LDB + j * MB];
     };
     if (nk > 0) {
-      load_slab(0);
-      store_slab(0, 0);
-      if (nk > 1) load_slab(BK);
+      load_slab(std::integral_constant<int, 0>{}, 0);
+      store_slab(std::integral_constant<int, 0>{}, 0, 0);
+      if (nk > 1) load_slab(std::integral_constant<int, DEPTH - 1>{}, BK);
+      if (DEPTH == 2 && nk > 2) load_slab(std::integral_constant<int, 0>{}, 2 * BK);
     }
     __syncthreads();
     if (nk > 0) load_frags(0, 0, 0);
-    for (int kt = 0; kt < nk; ++kt) {
-      const int cur = kt & 1;
+    // One slab; P = kt & 1 names its LDS buffer; slab s is staged in set
+    // s & 1 (two sets) or 0 (one set), and slab kt + 1 + DEPTH is loaded into
+    // the set that slab kt + 1 leaves.
+    auto slab = [&](auto par, int kt) __attribute__((always_inline)) {
+      constexpr int P = decltype(par)::value;
+      constexpr int cur = P;
       const bool more = kt + 1 < nk;
 #pragma unroll
       for (int kc = 0; kc < C; ++kc) {
         const int fs = kc & 1;
         if (C == 1 && more) {
-          store_slab(cur ^ 1, (kt + 1) * BK);
-          if (kt + 2 < nk) load_slab((kt + 2) * BK);
+          store_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, cur ^ 1, (kt + 1) * BK);
+          if (kt + 1 + DEPTH < nk) load_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, (kt + 1 + DEPTH) * BK);
         }
         if (kc + 1 < C) {
           load_frags(cur, kc + 1, fs ^ 1);
@@ -343,9 +360,8 @@ staged_gemm_kernel(GemmParams p) {
               acc[i][j] = mfma_block<MB>(bf[fs][j][s], af[fs][i][s], acc[i][j]);
         // Interleave the next chunk's LDS reads with this chunk's MFMAs, so a
         // wave issues its reads while its (dependent) MFMAs occupy the matrix
-        // pipe instead of before them (measured at 2048^3: 143.8 -> 134.5 us
-        // for the 128x128 4x4 tile).  One 32x32 block per wave: two MFMAs,
-        // two reads; more blocks: a read before each MFMA.
+        // pipe instead of before them.  One block per wave: two MFMAs, two
+        // reads; more blocks: a read before each MFMA.
         if constexpr (FM * FN == 1) {
 #pragma unroll
           for (int s = 0; s < 4; ++s) {
@@ -362,8 +378,8 @@ staged_gemm_kernel(GemmParams p) {
         __builtin_amdgcn_sched_barrier(0);
         if (C >= 2 && kc == MID && more) {
           __builtin_amdgcn_sched_barrier(0);
-          store_slab(cur ^ 1, (kt + 1) * BK);
-          if (kt + 2 < nk) load_slab((kt + 2) * BK);
+          store_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, cur ^ 1, (kt + 1) * BK);
+          if (kt + 1 + DEPTH < nk) load_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, (kt + 1 + DEPTH) * BK);
         }
       }
       // With an odd chunk count the next slab's first fragments landed in
@@ -376,7 +392,13 @@ staged_gemm_kernel(GemmParams p) {
 #pragma unroll
           for (int s = 0; s < 4; ++s) bf[0][j][s] = bf[1][j][s];
       }
+    };
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+      slab(std::integral_constant<int, 0>{}, kt);
+      slab(std::integral_constant<int, 1>{}, kt + 1);
     }
+    if (kt < nk) slab(std::integral_constant<int, 0>{}, kt);
   } else {
     // promote=0: fragments straight from global memory, no LDS, no barriers.
     const float *ag = A + (long)(wm * WTM + lr) * lda + 4 * lg;
@@ -418,7 +440,7 @@ staged_gemm_kernel(GemmParams p) {
   // with m = row lr of the block and n = 8*g + 4*lg (MB = 32, 4 groups) or
   // n = 4*lg (MB = 16, one group).
   constexpr int NG = MB == 32 ? 4 : 1;
-  auto group = [&](int i, int j, int g) {
+  auto group = [&](int i, int j, int g) __attribute__((always_inline)) {
     f32x4 v;
     v.x = acc[i][j][4 * g + 0];
     v.y = acc[i][j][4 * g + 1];
@@ -426,8 +448,8 @@ staged_gemm_kernel(GemmParams p) {
     v.w = acc[i][j][4 * g + 3];
     return v;
   };
-  auto row_of = [&](int i) { return m0 + wm * WTM + i * MB + lr; };
-  auto col_of = [&](int j, int g) { return (int)n0 + wn * WTN + j * MB + 8 * g + 4 * lg; };
+  auto row_of = [&](int i) __attribute__((always_inline)) { return m0 + wm * WTM + i * MB + lr; };
+  auto col_of = [&](int j, int g) __attribute__((always_inline)) { return (int)n0 + wn * WTN + j * MB + 8 * g + 4 * lg; };
 
   if (splits > 1) {
     // Split-K: this workgroup's partial sums go to slice `split` of the

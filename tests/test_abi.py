@@ -81,10 +81,16 @@ def test_registry_covers_config_space_and_resources():
     assert set(cm.config_space()) <= staged
     ablation = {e["cfg"] for e in reg if e["family"] == "staged" and e["cfg"][5:] != (1, 1)}
     assert (128, 64, 8, 4, 16, 0, 1) in ablation and (128, 64, 8, 4, 16, 1, 0) in ablation
-    # every LDS-staged configuration has a masked twin (mask-edges)
+    # every LDS-staged configuration whose threads stage <= 16 vectors per slab
+    # has a masked twin (mask-edges)
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("gen_instances", _lib.PKG / "csrc" / "gen_instances.py")
+    gi = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(gi)
     plain = {e["cfg"] for e in reg if e["family"] == "staged" and not e["name"].endswith("_masked")}
     masked = {e["cfg"] for e in reg if e["family"] == "staged" and e["name"].endswith("_masked")}
-    assert masked == {c for c in plain if c[5] == 1}
+    assert masked == {c for c in plain if c[5] == 1 and gi.staging_vectors(*c[:5], c[6]) <= 16}
+    assert (128, 128, 4, 4, 32, 1, 1) in masked and (64, 64, 2, 2, 64, 1, 1) in masked
     res = json.loads((_lib.PKG / "kernel_resources.json").read_text())
     for e in reg:
         assert e["name"] in res, e["name"]
