@@ -164,7 +164,7 @@ staged_gemm_kernel(GemmParams p) {
     using VT = typename std::conditional<VEC, f32x4, float>::type;
     // Staging sets in registers: two (loads two slabs ahead) when a thread
     // stages few vectors per slab, else one (loads 1.5 slabs ahead).
-    constexpr int DEPTH = (G::A_PER + G::B_PER) <= (MASK ? 4 : 8) ? 2 : 1;
+    constexpr int DEPTH = (G::A_PER + G::B_PER) <= 8 ? 2 : 1;
     VT ra[DEPTH][G::A_PER], rb[DEPTH][G::B_PER];
 
     // Masked instantiations (MASK = 1).  Rows of A at or past M and columns of B at
