@@ -97,7 +97,8 @@ def _block(tm, tn):
 
 
 def _lds_bytes(bm, bn, tm, tn, bk):
-    return 2 * (bm * (bk + 4) + bk * (bn + (8 if _block(tm, tn) == 32 else 4))) * 4
+    # two A and B tile buffers plus the tile's bias values
+    return (2 * (bm * (bk + 4) + bk * (bn + (8 if _block(tm, tn) == 32 else 4))) + bn) * 4
 
 
 def reference_space():

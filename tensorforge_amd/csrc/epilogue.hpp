@@ -12,10 +12,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // would return +0.0 for a NaN input, so the select is written out.
 __device__ __forceinline__ float relu_ieee(float x) { return (x > 0.0f || x != x) ? x : 0.0f; }
 
-// Applies the epilogue to four consecutive outputs C[m, n..n+3].
-__device__ __forceinline__ f32x4 apply_epi4(f32x4 v, const EpiParams &e, long m, int n) {
+// Applies the epilogue ops first.. to four consecutive outputs C[m, n..n+3]
+// (first = 1 when the caller has already added a prefetched bias).
+__device__ __forceinline__ f32x4 apply_epi4(f32x4 v, const EpiParams &e, long m, int n, int first = 0) {
 #pragma unroll
   for (int i = 0; i < kMaxEpi; ++i) {
+    if (i < first) continue;
     if (i >= e.nops) break;
     const int kind = e.kind[i];
     if (kind == EPI_BIAS) {

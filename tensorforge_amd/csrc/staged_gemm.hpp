@@ -29,8 +29,8 @@
 //    configurations); the slab loop is unrolled by two so buffer and set
 //    indices are compile-time.  The barrier
 //    sits before the slab's last chunk so those MFMAs hide the next slab's
-//    first LDS reads.  Each chunk's MFMAs are interleaved with the next
-//    chunk's fragment reads.  Row padding makes the b128 fragment reads and
+//    first LDS reads.  Each chunk's MFMAs are scheduled around the next
+//    chunk's fragment reads in a measured order.  Row padding makes the b128 fragment reads and
 //    the b32 B reads bank-conflict-free.
 //  * vectorize=1: 128-bit global loads and LDS accesses; vectorize=0: 32-bit.
 //  * promote=0: no LDS; each wave streams its fragments from global memory
@@ -104,7 +104,8 @@ struct StagedGemm {
   // or +4 (MB = 16) puts them in disjoint banks.
   static constexpr int LDB = BN + (MB == 32 ? 8 : 4);
   static constexpr int A_ELEMS = BM * LDA, B_ELEMS = BK * LDB;
-  static constexpr int LDS_BYTES = PROMOTE ? 2 * (A_ELEMS + B_ELEMS) * 4 : 0;
+  // Two A and B tile buffers, plus the tile's BN bias values.
+  static constexpr int LDS_BYTES = PROMOTE ? 2 * (A_ELEMS + B_ELEMS) * 4 + BN * 4 : 0;
   // Global -> register staging per thread and slab.
   static constexpr int VW = VEC ? 4 : 1;
   static constexpr int A_VECS = BM * BK / VW, B_VECS = BK * BN / VW;
@@ -157,6 +158,14 @@ staged_gemm_kernel(GemmParams p) {
       for (int r = 0; r < MB * MB / 64; ++r) acc[i][j][r] = 0.0f;
 
   const int nk = ke - kb;
+
+  // When the chain starts with bias_add (mbr, the residual block) the
+  // tile's BN bias values are staged in LDS during the prologue, so the
+  // epilogue reads them from LDS instead of starting on a cold global load.
+  // Not for split-K (the reduction applies the epilogue) or edge tiles
+  // (their columns may leave the matrix).
+  __shared__ __attribute__((aligned(16))) float bias_s[BN];
+  const bool bias_early = PROMOTE && splits == 1 && !edge && p.epi.nops > 0 && p.epi.kind[0] == EPI_BIAS;
 
   if constexpr (PROMOTE) {
     __shared__ __attribute__((aligned(16))) float As[2][G::A_ELEMS];
@@ -323,6 +332,8 @@ staged_gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) bf[slot][j][s] = bs[s * LDB + j * MB];
     };
+    if (bias_early && tid < BN / 4)
+      *reinterpret_cast<f32x4 *>(&bias_s[4 * tid]) = *reinterpret_cast<const f32x4 *>(p.epi.ptr[0] + n0 + 4 * tid);
     if (nk > 0) {
       load_slab(std::integral_constant<int, 0>{}, 0);
       store_slab(std::integral_constant<int, 0>{}, 0, 0);
@@ -358,21 +369,33 @@ staged_gemm_kernel(GemmParams p) {
 #pragma unroll
             for (int j = 0; j < FN; ++j)
               acc[i][j] = mfma_block<MB>(bf[fs][j][s], af[fs][i][s], acc[i][j]);
-        // Interleave the next chunk's LDS reads with this chunk's MFMAs, so a
-        // wave issues its reads while its (dependent) MFMAs occupy the matrix
-        // pipe instead of before them.  One block per wave: two MFMAs, two
-        // reads; more blocks: a read before each MFMA.
-        if constexpr (FM * FN == 1) {
+        // Order of this chunk's MFMAs and the next chunk's fragment reads,
+        // chosen by measurement on MI355X (main-loop shader cycles at 2048^3,
+        // launch times at 1024^3 and 4096^3 over 10 configurations):
+        //   one 32x32 block per wave:  2 MFMAs, all reads, 2 MFMAs;
+        //   one 16x16 block per wave:  2 MFMAs, 2 reads, repeated;
+        //   several blocks, <= 8 waves: all reads 2 MFMAs before the end;
+        //   several blocks, 16 waves:  MFMA, read, repeated.
+        constexpr int NM = 4 * FM * FN;  // MFMAs per chunk
+        if constexpr (FM * FN == 1 && MB == 32) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        } else if constexpr (FM * FN == 1) {
 #pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+          for (int s = 0; s < 2; ++s) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
           }
+        } else if constexpr (NT <= 512) {
+          __builtin_amdgcn_sched_group_barrier(0x008, NM - 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, FM + 4 * FN, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
         } else {
 #pragma unroll
-          for (int s = 0; s < 4 * FM * FN; ++s) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          for (int s = 0; s < NM; ++s) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -502,7 +525,9 @@ staged_gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
         const int n = col_of(j, g);
-        f32x4 v = apply_epi4(group(i, j, g), p.epi, m, n);
+        f32x4 v = bias_early
+                      ? apply_epi4(group(i, j, g) + *reinterpret_cast<const f32x4 *>(&bias_s[n - (int)n0]), p.epi, m, n, 1)
+                      : apply_epi4(group(i, j, g), p.epi, m, n);
         if constexpr (VEC) {
           *reinterpret_cast<f32x4 *>(crow + n) = v;
         } else {

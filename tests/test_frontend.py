@@ -214,7 +214,7 @@ def test_options_accept_braces_bools_and_print_script(capfd):
                     "{block-tile=128,128 thread-tile=8,8 tile-k=32 promote=true vectorize=1 print-script=1}")
     err = capfd.readouterr().err
     assert "tf_staged_b128x128_t8x8_k32" in err and "matmul+bias_add+relu" in err
-    assert k.launches()[0]["lds_bytes"] == 2 * (128 * 36 + 32 * 136) * 4
+    assert k.launches()[0]["lds_bytes"] == 2 * (128 * 36 + 32 * 136) * 4 + 128 * 4
 
 
 def test_staged_config_without_waves_is_rejected():
