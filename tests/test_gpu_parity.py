@@ -147,6 +147,43 @@ def test_launch_abi_matches_run():
     assert o.bitwise_diff(c.cpu().numpy(), out) == 0
 
 
+def test_concurrent_streams_with_separate_handles():
+    """Handles launched concurrently on their own streams (tf_launch's
+    contract: one handle per concurrent stream) give the bits each gives alone:
+    a plain staged kernel, a split-K kernel (private partial-sum workspace) and
+    the residual block (private intermediate h), two handles of each, 20
+    rounds on 6 streams."""
+    import torch
+    dev = torch.device("cuda:0")
+    cases = [("mbr", (512, 512, 512), STAGED.format(128, 128, 8, 4, 32)),
+             ("mbr", (512, 512, 512), STAGED.format(64, 128, 4, 4, 32) + " split-k=4"),
+             ("resmlp", (256, 128, 512), STAGED.format(64, 64, 4, 4, 32))]
+    jobs = []
+    for wl, (m, n, k), opts in cases:
+        ins = tc.make_inputs(wl, m, n, k)
+        bufs = [torch.from_numpy(np.ascontiguousarray(v)).to(dev) for v in ins.values()]
+        for _ in range(2):
+            kern = _lib.Kernel(tc.gen_mlir(wl, m, n, k), opts, "t.mlir")
+            out = torch.full((m, n), float("nan"), device=dev)
+            jobs.append((kern, [b.data_ptr() for b in bufs] + [out.data_ptr()], out, bufs))
+    cur = torch.cuda.current_stream()
+    for kern, ptrs, out, _ in jobs:
+        kern.launch(ptrs, cur.cuda_stream)
+    torch.cuda.synchronize()
+    alone = [out.cpu().numpy().copy() for _, _, out, _ in jobs]
+    for _, _, out, _ in jobs:
+        out.fill_(float("nan"))
+    streams = [torch.cuda.Stream() for _ in jobs]
+    torch.cuda.synchronize()
+    for _ in range(20):
+        for (kern, ptrs, _, _), s in zip(jobs, streams):
+            kern.launch(ptrs, s.cuda_stream)
+    torch.cuda.synchronize()
+    for (_, _, out, _), want in zip(jobs, alone):
+        assert not np.isnan(want).any()
+        assert o.bitwise_diff(out.cpu().numpy(), want) == 0
+
+
 def test_deterministic():
     opts = STAGED.format(128, 64, 8, 4, 16)
     _, a = run_prog("mbr", 512, 512, 512, opts)
