@@ -201,6 +201,19 @@ staged_gemm_kernel(GemmParams p) {
       __builtin_memcpy(&v, src, sizeof(VT));
       return v;
     };
+    // Per-thread part of each B staging address: a slab then adds only the
+    // uniform k0 * ldb (one scalar product) instead of recomputing
+    // (k0 + r) * ldb per thread in 64-bit vector arithmetic.
+    // (The masked twins' clamped loads do the same with 32-bit offsets.)
+    const float *b_src[G::B_PER];
+    int b_off[G::B_PER];
+#pragma unroll
+    for (int it = 0; it < G::B_PER; ++it) {
+      const int q = tid + it * NT;
+      const int r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
+      b_src[it] = B + r * ldb + c;
+      b_off[it] = (kbi + r) * (int)ldb + (n0i + c < Ni ? n0i + c : Ni - VW);
+    }
     // `sc` is std::integral_constant<int, set>: the staging set is compile-time
     // even where the lambda is not inlined, so the registers stay registers.
     auto load_slab = [&](auto sc, int k0) __attribute__((always_inline)) {
@@ -219,7 +232,7 @@ staged_gemm_kernel(GemmParams p) {
           const int q = tid + it * NT;
           if (G::B_VECS % NT == 0 || q < G::B_VECS) {
             const int r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
-            rb[set][it] = *reinterpret_cast<const VT *>(B + (k0 + r) * ldb + c);
+            rb[set][it] = *reinterpret_cast<const VT *>(b_src[it] + k0 * ldb);
           }
         }
       } else if (!guarded(k0)) {
@@ -235,9 +248,7 @@ staged_gemm_kernel(GemmParams p) {
         for (int it = 0; it < G::B_PER; ++it) {
           const int q = tid + it * NT;
           if (G::B_VECS % NT == 0 || q < G::B_VECS) {
-            const int r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
-            const int gn = n0i + c < Ni ? n0i + c : Ni - VW;
-            rb[set][it] = load16(p.B + ((kbi + k0 + r) * (int)ldb + gn));
+            rb[set][it] = load16(p.B + (b_off[it] + k0 * (int)ldb));
           }
         }
       } else {
