@@ -27,11 +27,13 @@
 //    middle of slab t+2), so the LDS writes do not wait on HBM latency under
 //    full-chip load (one set, 1.5 slabs ahead, for the register-heavy
 //    configurations); the slab loop is unrolled by two so buffer and set
-//    indices are compile-time.  The barrier
-//    sits before the slab's last chunk so those MFMAs hide the next slab's
-//    first LDS reads.  Each chunk's MFMAs are scheduled around the next
-//    chunk's fragment reads in a measured order.  Row padding makes the b128 fragment reads and
-//    the b32 B reads bank-conflict-free.
+//    indices are compile-time.  The barrier sits before the slab's last
+//    chunk so those MFMAs hide the next slab's first LDS reads.  Each
+//    chunk's MFMAs are scheduled around the next chunk's fragment reads in a
+//    measured order.  Row padding makes the b128 fragment reads and the b32
+//    B reads bank-conflict-free.
+//  * Epilogue in registers: bias (staged in LDS during the prologue when the
+//    chain starts with bias_add), IEEE relu, residual add; 128-bit stores.
 //  * vectorize=1: 128-bit global loads and LDS accesses; vectorize=0: 32-bit.
 //  * promote=0: no LDS; each wave streams its fragments from global memory
 //    (through L2), the reference's "+tiling" rung (bench/stage9_ablation.py:23-28).
