@@ -184,6 +184,39 @@ def test_concurrent_streams_with_separate_handles():
         assert o.bitwise_diff(out.cpu().numpy(), want) == 0
 
 
+def test_launch_replays_from_a_hip_graph():
+    """tf_launch enqueues only kernel launches on the caller's stream (no
+    memsets; a handle allocates its workspace and intermediates on its first
+    launch), so after one eager launch it can be captured into a HIP graph:
+    a plain staged kernel, split-K (GEMM + reduction) and the residual block
+    (two layers and an intermediate) replay the eager bits five times, with
+    eager work and synchronisation between the replays."""
+    import torch
+    dev = torch.device("cuda:0")
+    cases = [("mbr", (512, 512, 512), STAGED.format(128, 128, 8, 4, 32)),
+             ("mbr", (512, 512, 512), STAGED.format(64, 128, 4, 4, 32) + " split-k=4"),
+             ("resmlp", (256, 128, 512), STAGED.format(64, 64, 4, 4, 32))]
+    for wl, (m, n, k), opts in cases:
+        ins = tc.make_inputs(wl, m, n, k)
+        bufs = [torch.from_numpy(np.ascontiguousarray(v)).to(dev) for v in ins.values()]
+        kern = _lib.Kernel(tc.gen_mlir(wl, m, n, k), opts, "t.mlir")
+        out = torch.full((m, n), float("nan"), device=dev)
+        ptrs = [b.data_ptr() for b in bufs] + [out.data_ptr()]
+        kern.launch(ptrs, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        want = out.cpu().numpy().copy()
+        assert not np.isnan(want).any()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            kern.launch(ptrs, torch.cuda.current_stream().cuda_stream)
+        for rep in range(5):
+            out.fill_(float("nan"))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert o.bitwise_diff(out.cpu().numpy(), want) == 0, (wl, opts, rep)
+
+
 def test_deterministic():
     opts = STAGED.format(128, 64, 8, 4, 16)
     _, a = run_prog("mbr", 512, 512, 512, opts)
