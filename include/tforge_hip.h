@@ -108,7 +108,8 @@ typedef struct {
 
 const char *tf_last_error(void);
 
-/* Device 0 facts (the reference runner also uses device 0). */
+/* Device 0 facts (the reference runner also uses device 0 and reports its
+ * name and driver in the JSON line, runners/gpu/tforge-gpu-bench.cu:367-381). */
 int tf_device_info(tf_device_info_t *out);
 
 /* Parse + verify `program` (tforge text, diagnostics name `source_name`),
@@ -122,10 +123,16 @@ int tf_device_info(tf_device_info_t *out);
 int tf_compile(const char *source_name, const char *program, const char *options, tf_kernel_t **out);
 void tf_kernel_free(tf_kernel_t *k);
 
+/* The compiled program's launches (one, or two for the residual block) and
+ * buffers: what the reference reads back from launch.json and the runner's
+ * --grid/--block/--args flags (python/tforge_gpu.py:42-51, 88-90;
+ * runners/gpu/tforge-gpu-bench.cu:20-24, 92-140). */
 int tf_kernel_num_launches(const tf_kernel_t *k);
 int tf_kernel_launch_info(const tf_kernel_t *k, int launch, tf_launch_info_t *out);
 int tf_kernel_num_buffers(const tf_kernel_t *k); /* entry arguments + 1 result */
 int tf_kernel_buffer_info(const tf_kernel_t *k, int index, tf_buffer_info_t *out);
+/* Resources and occupancy of one launch: the runner's --info-only
+ * (runners/gpu/tforge-gpu-bench.cu:278-291). */
 int tf_kernel_info(const tf_kernel_t *k, int launch, tf_kernel_resources_t *out);
 
 /* Kernel ABI: enqueue every launch of the program on `stream` (a hipStream_t,
@@ -157,12 +164,14 @@ int tf_bench(tf_kernel_t *k, int mode, const long long *logical_mnk, const float
              unsigned seed, int warmup, int reps, int flush, tf_bench_result_t *out);
 
 /* Per-rep event times (ms) of the last tf_bench on this handle, up to `cap`
- * values; returns the count. */
+ * values; returns the count.  No counterpart in the reference (its runner
+ * prints only median/min/std); for callers that want the distribution. */
 int tf_bench_samples(const tf_kernel_t *k, double *out_ms, int cap);
 
 /* Registry introspection: number of ahead-of-time instantiations and the
  * staged configuration of entry i (family, bm, bn, tm, tn, bk, promote,
- * vectorize) -- what the autotuner may select. */
+ * vectorize) -- what the autotuner may select.  No counterpart in the
+ * reference, which generates each kernel on demand. */
 int tf_registry_size(void);
 int tf_registry_entry(int i, int *family, int *cfg7, char *name, int name_cap);
 
