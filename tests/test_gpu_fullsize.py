@@ -1,0 +1,115 @@
+"""Every BASELINE configuration at its full size, through tf_launch, with the
+options the benchmarks use (autotuned, else the cost model's pick).
+
+A full FP64 reference of the largest problems costs minutes on the host, so
+these tests check properties that hold for any summation order and are
+therefore exact at any size, plus the reference's bound on sampled rows:
+
+  * scaling: doubling A and the bias (and x, b1, b2 of the residual block)
+    doubles every output bit for bit -- products and sums scale exactly by a
+    power of two, relu(2z) = 2 relu(z);
+  * row permutation: permuting the rows of A (of x) permutes the output rows
+    bit for bit -- each output row's arithmetic does not depend on its tile;
+  * column permutation: permuting the columns of B together with the bias
+    permutes the output columns bit for bit;
+  * 32 sampled rows against the FP64 reference with the reference's bound
+    (python/tforge_gpu.py:134-145) and exact ReLU masks, or the composed
+    bound of the residual block.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+from tensorforge_amd import _lib
+from tensorforge_amd import costmodel as cm
+from tensorforge_amd import tforge_cpu as tc
+from tensorforge_amd import tforge_gpu as tg
+
+pytestmark = pytest.mark.gpu
+
+# examples/mbr.mlir, the 2048^3 headline, plain matmul
+# 512..8192^3, the rectangular MLP layers (skinny and short-K included).
+CASES = [("mbr", 256, 256, 128), ("mbr", 2048, 2048, 2048),
+         ("matmul", 512, 512, 512), ("matmul", 1024, 1024, 1024), ("matmul", 2048, 2048, 2048),
+         ("matmul", 4096, 4096, 4096), ("matmul", 8192, 8192, 8192),
+         ("mbr", 8192, 1024, 4096), ("mbr", 1024, 8192, 4096), ("mbr", 64, 4096, 4096), ("mbr", 4096, 4096, 256)]
+
+
+def _torch():
+    import torch
+    return torch, torch.device("cuda:0")
+
+
+def _bits(t):
+    torch, _ = _torch()
+    return t.contiguous().view(torch.int32)
+
+
+@pytest.mark.parametrize("workload,m,n,k", CASES)
+def test_full_size_properties(workload, m, n, k):
+    torch, dev = _torch()
+    opts = cm.tuned_options(workload, m, n, k)
+    kern = _lib.Kernel(tc.gen_mlir(workload, m, n, k), opts, "t.mlir")
+    stream = torch.cuda.current_stream().cuda_stream
+    g = torch.Generator(device=dev).manual_seed(1234)
+    a = torch.rand(m, k, device=dev, generator=g) * 2 - 1
+    b = torch.rand(k, n, device=dev, generator=g) * 2 - 1
+    bias = torch.rand(n, device=dev, generator=g) * 2 - 1
+    mbr = workload == "mbr"
+
+    def run(a_, b_, bias_):
+        out = torch.full((m, n), float("nan"), device=dev)
+        ins = [a_.contiguous(), b_.contiguous()] + ([bias_.contiguous()] if mbr else [])
+        kern.launch([t.data_ptr() for t in ins] + [out.data_ptr()], stream)
+        torch.cuda.synchronize()
+        return out
+
+    out = run(a, b, bias)
+    assert not torch.isnan(out).any()
+    assert torch.equal(_bits(run(2 * a, b, 2 * bias)), _bits(2 * out))
+    rp = torch.randperm(m, device=dev, generator=g)
+    assert torch.equal(_bits(run(a[rp], b, bias)), _bits(out[rp]))
+    cp = torch.randperm(n, device=dev, generator=g)
+    assert torch.equal(_bits(run(a, b[:, cp], bias[cp])), _bits(out[:, cp]))
+
+    rows = np.sort(np.random.default_rng(7).choice(m, size=min(32, m), replace=False))
+    ins = {"a": a[rows].cpu().numpy(), "b": b.cpu().numpy()}
+    if mbr:
+        ins["bias"] = bias.cpu().numpy()
+    got = out[rows].cpu().numpy()
+    ref, bound = o.fp64_reference(workload, ins)
+    assert o.e1_metrics(got, ref, bound)["max_err_over_bound"] <= 1.0
+    if mbr:
+        assert o.mask_mismatches(got, o.preactivation64(ins), bound) == 0
+
+
+def test_full_size_residual_block():
+    """The residual block at its BASELINE size (x 4096x2048, W1 2048x8192,
+    W2 8192x2048) with the measured best tiles."""
+    torch, dev = _torch()
+    m, n, k = 4096, 2048, 8192
+    opts = "block-tile=128,256 thread-tile=8,4 tile-k=32 promote=1 vectorize=1"
+    kern = _lib.Kernel(tc.gen_mlir("resmlp", m, n, k), opts, "t.mlir")
+    stream = torch.cuda.current_stream().cuda_stream
+    host = tc.make_inputs("resmlp", m, n, k)
+    x, w1, b1, w2, b2 = (torch.from_numpy(np.ascontiguousarray(host[s])).to(dev) for s in ("x", "w1", "b1", "w2", "b2"))
+
+    def run(x_, b1_, b2_):
+        y = torch.full((m, n), float("nan"), device=dev)
+        kern.launch([t.contiguous().data_ptr() for t in (x_, w1, b1_, w2, b2_)] + [y.data_ptr()], stream)
+        torch.cuda.synchronize()
+        return y
+
+    y = run(x, b1, b2)
+    assert not torch.isnan(y).any()
+    assert torch.equal(_bits(run(2 * x, 2 * b1, 2 * b2)), _bits(2 * y))
+    g = torch.Generator(device=dev).manual_seed(5)
+    rp = torch.randperm(m, device=dev, generator=g)
+    xp = x[rp].contiguous()
+    assert torch.equal(_bits(run(xp, b1, b2)), _bits(y[rp]))
+
+    rows = np.sort(np.random.default_rng(7).choice(m, size=32, replace=False))
+    sub = dict(host)
+    sub["x"] = host["x"][rows]
+    assert tg._resmlp_check(sub, y[rows].cpu().numpy())["pass"]
