@@ -174,8 +174,8 @@ def _resmlp_check(ins, out):
     y = np.maximum(z2, 0.0) + x
     bound = ez + tc.F32_EPS * (np.abs(y) + ez) + np.finfo(np.float32).tiny
     err = np.abs(out.astype(np.float64) - y)
-    res = {"nan_count": int(np.isnan(out).sum()), "max_abs_err": float(np.nanmax(err)),
-           "err_over_bound": float(np.nanmax(err / bound))}
+    res = {"nan_count": int(np.isnan(out).sum()), "max_abs_err": float(np.nanmax(err)) if err.size else 0.0,
+           "err_over_bound": float(np.nanmax(err / bound)) if err.size else 0.0}
     res["pass"] = res["nan_count"] == 0 and res["err_over_bound"] <= 1.0
     return res
 
@@ -203,7 +203,7 @@ def check(workload, m, n, k, kdir=None, launch=None, mode="kernel", seed=1234):
         exact = bool(np.array_equal(out.view(np.uint32), np.ascontiguousarray(ref, np.float32).view(np.uint32)))
         return {"pass": exact, "nan_count": int(np.isnan(out).sum()),
                 "err_over_bound": 0.0 if exact else float("inf"),
-                "max_abs_err": float(np.max(np.abs(out.astype(np.float64) - ref)))}, out
+                "max_abs_err": float(np.max(np.abs(out.astype(np.float64) - ref))) if out.size else 0.0}, out
     if workload == "resmlp":
         return _resmlp_check(ins, out), out
     return _bound_check(workload, ins, out, k), out

@@ -217,6 +217,39 @@ def test_launch_replays_from_a_hip_graph():
             assert o.bitwise_diff(out.cpu().numpy(), want) == 0, (wl, opts, rep)
 
 
+@pytest.mark.parametrize("workload,shape,opts", [
+    ("mbr", (0, 4, 4), "block-tile=16,16 thread-tile=1,1"),
+    ("mbr", (4, 0, 4), "block-tile=16,16 thread-tile=1,1"),
+    ("mbr", (5, 4, 0), "block-tile=16,16 thread-tile=1,1"),
+    ("matmul", (8, 8, 0), "block-tile=16,16 thread-tile=1,1"),
+    ("mbr", (0, 64, 64), STAGED.format(64, 64, 4, 4, 32)),
+    ("mbr", (64, 64, 0), STAGED.format(64, 64, 4, 4, 32)),
+    ("mbr", (65, 70, 0), STAGED.format(64, 64, 4, 4, 32) + " mask-edges=1"),
+    ("matmul", (64, 128, 0), STAGED.format(64, 64, 2, 2, 64)),
+])
+def test_empty_dimensions(workload, shape, opts):
+    """Zero-sized M or N launch nothing; K = 0 is an empty sum, +0.0, so the
+    output is the epilogue of zero: relu(0 + bias) for mbr, +0.0 for matmul."""
+    m, n, k = shape
+    ins = o.make_inputs(workload, m, n, k)
+    kern = _lib.Kernel(tc.gen_mlir(workload, m, n, k), opts, "t.mlir")
+    out = np.full((m, n), np.nan, np.float32)
+    kern.run([np.ascontiguousarray(v) for v in ins.values()], out)
+    if m and n:
+        want = np.zeros((m, n), np.float32)
+        if workload == "mbr":
+            want = o.epilogue(want, ins["bias"], relu=True)
+        assert o.bitwise_diff(out, want) == 0
+
+
+@pytest.mark.parametrize("shape", [(0, 8), (8, 0)])
+def test_empty_element_op(shape):
+    m, n = shape
+    d, launch = tg.compile_kernel("relu", m, n, None, "block-tile=4,256 thread-tile=1,4", tag="test")
+    res, out = tg.check("relu", m, n, None, d, launch)
+    assert res["pass"] and out.shape == (m, n)
+
+
 def test_deterministic():
     opts = STAGED.format(128, 64, 8, 4, 16)
     _, a = run_prog("mbr", 512, 512, 512, opts)
