@@ -346,6 +346,25 @@ def test_masked_edges_equal_pad_path_bits(workload, shape, cfg, extra):
     assert_bound(workload, ins, masked)
 
 
+NARROW_SHAPES = [(5, 2, 3), (33, 3, 70), (70, 6, 9), (65, 7, 2), (2, 130, 5), (129, 1, 257)]
+
+
+@pytest.mark.parametrize("workload", ["mbr", "matmul"])
+@pytest.mark.parametrize("shape", NARROW_SHAPES)
+@pytest.mark.parametrize("cfg", [(64, 64, 2, 2, 64), (64, 64, 4, 4, 32)])
+def test_masked_narrow_shapes_equal_pad_path_bits(workload, shape, cfg):
+    """Rows narrower than one 16-byte vector (N < 4: every slab guarded),
+    unaligned rows (N % 4 != 0), K below one k-chunk, on 16x16 and 32x32
+    MFMA blocks: the pad path's bits and the bound."""
+    m, n, k = shape
+    opts = STAGED.format(*cfg)
+    ins = o.make_inputs(workload, m, n, k)
+    _, masked = run_prog(workload, m, n, k, opts + " mask-edges=1", ins=ins)
+    _, padded = run_prog(workload, m, n, k, opts, ins=ins, logical=cm.padded(cfg, m, n, k))
+    assert o.bitwise_diff(masked, padded) == 0
+    assert_bound(workload, ins, masked)
+
+
 def test_masked_resmlp_ragged():
     """Residual block at a shape that is not a multiple of the tiles."""
     m, n, k = 200, 72, 136
