@@ -1,0 +1,73 @@
+"""A seeded random sweep over the staged path's option space, through tf_run.
+
+48 draws (seed 2026): workload mbr or matmul; each of M, N, K uniform in
+1..700; a configuration from the 224-entry CDNA4 space; a split-K factor from
+1, 2, 3, 5, 8 (at most the problem's K slabs); mask-edges on or off (on only
+for configurations that have a masked twin).  Every draw meets the reference's
+bar: no NaN in the NaN-prefilled output, max err/bound <= 1 against the FP64
+reference (python/tforge_gpu.py:134-145), exact ReLU masks.  A masked draw
+also equals the pad path (zero-padded copies through the unmasked kernel,
+the reference runner's method) bit for bit.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+from tensorforge_amd import _lib
+from tensorforge_amd import costmodel as cm
+from tensorforge_amd import tforge_cpu as tc
+
+pytestmark = pytest.mark.gpu
+
+STAGED = "block-tile={},{} thread-tile={},{} tile-k={} promote=1 vectorize=1"
+
+
+def _draws(count=48, seed=2026):
+    rng = np.random.default_rng(seed)
+    space = list(cm.config_space())
+    twins = {tuple(e["cfg"][:5]) for e in _lib.registry() if e["family"] == "staged" and e["name"].endswith("_masked")}
+    out = []
+    while len(out) < count:
+        wl = ("mbr", "matmul")[rng.integers(2)]
+        m, n, k = (int(v) for v in rng.integers(1, 701, size=3))
+        cfg = tuple(int(v) for v in space[rng.integers(len(space))])
+        masked = bool(rng.integers(2)) and cfg in twins
+        kk = k if masked else cm.padded(cfg, m, n, k)[2]
+        slabs = -(-kk // cfg[4])
+        split = int(rng.choice([1, 2, 3, 5, 8]))
+        if split > slabs:
+            split = 1
+        out.append((wl, (m, n, k), cfg, split, masked))
+    return out
+
+
+DRAWS = _draws()
+
+
+def _run(workload, m, n, k, options, ins, logical=None):
+    pm, pn, pk = logical or (m, n, k)
+    kern = _lib.Kernel(tc.gen_mlir(workload, pm, pn, pk), options, "t.mlir")
+    out = np.empty((m, n), np.float32)
+    kern.run([np.ascontiguousarray(v) for v in ins.values()], out,
+             logical=None if logical is None or tuple(logical) == (m, n, k) else (m, n, k))
+    return out
+
+
+@pytest.mark.parametrize("workload,shape,cfg,split,masked", DRAWS,
+                         ids=[f"{d[0]}-{'x'.join(map(str, d[1]))}-b{d[2][0]}x{d[2][1]}-t{d[2][2]}x{d[2][3]}"
+                              f"-k{d[2][4]}-s{d[3]}{'-masked' if d[4] else ''}" for d in DRAWS])
+def test_random_draw(workload, shape, cfg, split, masked):
+    m, n, k = shape
+    opts = STAGED.format(*cfg) + (f" split-k={split}" if split > 1 else "")
+    ins = o.make_inputs(workload, m, n, k)
+    print(f"draw {workload} {shape} {opts} masked={masked}", flush=True)
+    padded = _run(workload, m, n, k, opts, ins, logical=cm.padded(cfg, m, n, k))
+    ref, bound = o.fp64_reference(workload, ins)
+    for out in ([padded, _run(workload, m, n, k, opts + " mask-edges=1", ins)] if masked else [padded]):
+        assert not np.isnan(out).any()
+        eob = o.e1_metrics(out, ref, bound)["max_err_over_bound"]
+        assert eob <= 1.0, eob
+        if workload == "mbr":
+            assert o.mask_mismatches(out, o.preactivation64(ins), bound) == 0
+        assert o.bitwise_diff(out, padded) == 0
