@@ -30,17 +30,17 @@ bool Type::static_shape() const {
   return true;
 }
 
-int64_t Type::numel() const {
+// Product of dimensions, saturating at INT64_MAX (shapes are user text).
+static int64_t product(const std::vector<int64_t> &dims, size_t count) {
   int64_t n = 1;
-  for (int64_t d : shape) n *= d;
+  for (size_t i = 0; i < count; ++i)
+    if (__builtin_mul_overflow(n, dims[i], &n)) return INT64_MAX;
   return n;
 }
 
-int64_t Buffer::numel() const {
-  int64_t n = 1;
-  for (int64_t d : shape) n *= d;
-  return n;
-}
+int64_t Type::numel() const { return product(shape, shape.size()); }
+
+int64_t Buffer::numel() const { return product(shape, shape.size()); }
 
 std::string format_error(const std::string &source_name, Loc loc, const std::string &msg) {
   std::ostringstream os;
@@ -161,9 +161,17 @@ struct Parser {
             continue;
           }
           if (i < lx.s.size() && std::isdigit((unsigned char)lx.s[i])) {
+            const Loc dl = lx.loc();
             size_t j = i;
-            while (j < lx.s.size() && std::isdigit((unsigned char)lx.s[j])) ++j;
-            t.shape.push_back(std::stoll(lx.s.substr(i, j - i)));
+            int64_t d = 0;
+            bool too_big = false;
+            for (; j < lx.s.size() && std::isdigit((unsigned char)lx.s[j]); ++j) {
+              const int64_t digit = lx.s[j] - '0';
+              if (d > (INT64_MAX - digit) / 10) too_big = true;
+              else d = d * 10 + digit;
+            }
+            if (too_big) return fail(dl, "invalid dimension");  // past int64, as MLIR's type parser says
+            t.shape.push_back(d);
             lx.adv(j - i);
             if (!expect("x")) return false;
             continue;
@@ -678,8 +686,7 @@ bool plan_program(const Program &p, const Options &o, Plan &plan, std::string &e
   };
   auto flat2d = [](const std::vector<int64_t> &s, int64_t &m, int64_t &n) {
     n = s.empty() ? 1 : s.back();
-    m = 1;
-    for (size_t i = 0; i + 1 < s.size(); ++i) m *= s[i];
+    m = s.empty() ? 1 : product(s, s.size() - 1);
   };
 
   for (const Op &op : p.ops) {
@@ -758,6 +765,16 @@ bool plan_program(const Program &p, const Options &o, Plan &plan, std::string &e
     return false;
   }
   close();
+  // The kernels take M, N and K as 32-bit integers (offsets are 64-bit, so a
+  // matrix may still hold more than 2^31 elements).
+  for (const Stage &st : plan.stages)
+    if (st.M > INT32_MAX || st.N > INT32_MAX || st.K > INT32_MAX) {
+      err = format_error(p.source_name, st.loc,
+                         "tforge-gpu-pipeline: dimensions above 2^31 - 1 are not supported (M = " +
+                             std::to_string(st.M) + ", N = " + std::to_string(st.N) + ", K = " +
+                             std::to_string(st.K) + ")");
+      return false;
+    }
   return true;
 }
 

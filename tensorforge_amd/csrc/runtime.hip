@@ -10,7 +10,10 @@
 #include <cstdlib>
 #include <cstring>
 #include <functional>
+#include <memory>
+#include <new>
 #include <random>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -25,6 +28,21 @@ thread_local std::string g_err;
 int fail(int code, const std::string &m) {
   g_err = m;
   return code;
+}
+
+// Runs an entry point's body; a C++ exception (an allocation failure, say)
+// becomes an error code and message instead of unwinding into the caller.
+template <typename F>
+int guarded(F &&body) {
+  try {
+    return body();
+  } catch (const std::bad_alloc &) {
+    return fail(TF_E_ARG, "out of host memory");
+  } catch (const std::exception &e) {
+    return fail(TF_E_ARG, std::string("internal error: ") + e.what());
+  } catch (...) {
+    return fail(TF_E_ARG, "internal error");
+  }
 }
 
 #define TF_HIP(x)                                                                                  \
@@ -589,29 +607,23 @@ int tf_device_info(tf_device_info_t *out) {
   return TF_OK;
 }
 
-int tf_compile(const char *source_name, const char *program, const char *options, tf_kernel_t **out) {
+static int compile_impl(const char *source_name, const char *program, const char *options, tf_kernel_t **out) {
   if (!program || !out) return fail(TF_E_ARG, "null program or output handle");
   *out = nullptr;
-  auto *k = new tf_kernel();
+  std::unique_ptr<tf_kernel> k(new tf_kernel());
   std::string err;
   const std::string src = source_name ? source_name : "<input>";
   if (!tff::parse_program(program, src, k->prog, err) || !tff::verify_program(k->prog, err)) {
-    delete k;
     return fail(TF_E_PARSE, err);
   }
   if (!tff::parse_options(options ? options : "", k->opts, err)) {
-    delete k;
     return fail(TF_E_OPTIONS, err);
   }
   if (!tff::plan_program(k->prog, k->opts, k->plan, err)) {
-    delete k;
     return fail(TF_E_PLAN, err);
   }
-  int rc = select_launches(k);
-  if (rc) {
-    delete k;
-    return rc;
-  }
+  int rc = select_launches(k.get());
+  if (rc) return rc;
   if (k->opts.print_script || k->opts.print_after_each) {
     for (size_t s = 0; s < k->plan.stages.size(); ++s) {
       const tff::Stage &st = k->plan.stages[s];
@@ -621,7 +633,7 @@ int tf_compile(const char *source_name, const char *program, const char *options
                    (long long)st.N, (long long)st.K);
     }
   }
-  *out = k;
+  *out = k.release();
   return TF_OK;
 }
 
@@ -698,7 +710,7 @@ int tf_kernel_info(const tf_kernel_t *k, int launch, tf_kernel_resources_t *out)
   return TF_OK;
 }
 
-int tf_launch(tf_kernel_t *k, void *const *device_buffers, void *stream) {
+static int launch_impl(tf_kernel_t *k, void *const *device_buffers, void *stream) {
   if (!k || !device_buffers) return fail(TF_E_ARG, "null kernel or buffers");
   std::vector<void *> ptrs;
   int rc = pointer_table(k, device_buffers, ptrs);
@@ -710,7 +722,8 @@ int tf_launch(tf_kernel_t *k, void *const *device_buffers, void *stream) {
   return TF_OK;
 }
 
-int tf_run(tf_kernel_t *k, int mode, const long long *logical_mnk, const float *const *host_inputs, float *host_out) {
+static int run_impl(tf_kernel_t *k, int mode, const long long *logical_mnk, const float *const *host_inputs,
+                    float *host_out) {
   if (!k || !host_inputs || !host_out) return fail(TF_E_ARG, "null kernel, inputs or output");
   Exec ex;
   int rc = prepare(k, mode, logical_mnk, host_inputs, 0, ex);
@@ -727,8 +740,8 @@ int tf_run(tf_kernel_t *k, int mode, const long long *logical_mnk, const float *
   return TF_OK;
 }
 
-int tf_bench(tf_kernel_t *k, int mode, const long long *logical_mnk, const float *const *host_inputs, unsigned seed,
-             int warmup, int reps, int flush, tf_bench_result_t *out) {
+static int bench_impl(tf_kernel_t *k, int mode, const long long *logical_mnk, const float *const *host_inputs,
+                      unsigned seed, int warmup, int reps, int flush, tf_bench_result_t *out) {
   if (!k || !out || warmup < 0 || reps < 1) return fail(TF_E_ARG, "bad bench arguments");
   Exec ex;
   int rc = prepare(k, mode, logical_mnk, host_inputs, seed, ex);
@@ -819,6 +832,25 @@ int tf_registry_entry(int i, int *family, int *cfg7, char *name, int name_cap) {
   }
   if (name && name_cap > 0) std::snprintf(name, name_cap, "%s", e.name);
   return TF_OK;
+}
+
+// The entry points above that parse user text or allocate host memory run
+// behind this guard: no C++ exception crosses the C ABI.
+int tf_compile(const char *source_name, const char *program, const char *options, tf_kernel_t **out) {
+  return guarded([&] { return compile_impl(source_name, program, options, out); });
+}
+
+int tf_launch(tf_kernel_t *k, void *const *device_buffers, void *stream) {
+  return guarded([&] { return launch_impl(k, device_buffers, stream); });
+}
+
+int tf_run(tf_kernel_t *k, int mode, const long long *logical_mnk, const float *const *host_inputs, float *host_out) {
+  return guarded([&] { return run_impl(k, mode, logical_mnk, host_inputs, host_out); });
+}
+
+int tf_bench(tf_kernel_t *k, int mode, const long long *logical_mnk, const float *const *host_inputs, unsigned seed,
+             int warmup, int reps, int flush, tf_bench_result_t *out) {
+  return guarded([&] { return bench_impl(k, mode, logical_mnk, host_inputs, seed, warmup, reps, flush, out); });
 }
 
 }  // extern "C"

@@ -146,6 +146,29 @@ def test_notpadded_located_error():
                    "multiples of the block and K tiles")
 
 
+def test_dimension_limits():
+    """A dimension past int64 is a located "invalid dimension" (MLIR's type
+    parser message); one past 2^31 - 1 parses but the kernels take 32-bit M, N
+    and K, so planning refuses it at the op; 2^31 - 1 itself is accepted."""
+    prog = tc.gen_mlir("relu", 4, 8).replace("4x8", "99999999999999999999x8", 1)
+    line = next(i for i, l in enumerate(prog.splitlines(), 1) if "99999999999999999999" in l)
+    col = prog.splitlines()[line - 1].index("99999999999999999999") + 1
+    assert compile_err(prog) == f"t.mlir:{line}:{col}: error: invalid dimension"
+    big = tc.gen_mlir("mbr", 2147483648, 16, 8)
+    line = next(i for i, l in enumerate(big.splitlines(), 1) if "tforge.matmul" in l)
+    col = big.splitlines()[line - 1].index("tforge.matmul") + 1
+    assert compile_err(big) == (f"t.mlir:{line}:{col}: error: tforge-gpu-pipeline: dimensions above 2^31 - 1 are "
+                                "not supported (M = 2147483648, N = 16, K = 8)")
+    assert "dimensions above" in compile_err(tc.gen_mlir("matmul", 4, 4, 1 << 40))
+    assert "dimensions above" in compile_err(tc.gen_mlir("relu", 1 << 31, 4))
+    # rank-3 element op: the leading dimensions flatten to M = 2^33 (no overflow on the way)
+    rank3 = tc.gen_mlir("relu", 4, 8).replace("4x8", "65536x131072x8")
+    assert "dimensions above" in compile_err(rank3)
+    huge3 = tc.gen_mlir("relu", 4, 8).replace("4x8", "9223372036854775807x9223372036854775807x8")
+    assert "dimensions above" in compile_err(huge3)
+    assert _lib.Kernel(tc.gen_mlir("mbr", 2147483647, 16, 8), "").launches()[0]["grid"] == [1, 134217728, 1]
+
+
 def test_tile_k_needs_a_matmul():
     err = compile_err(tc.gen_mlir("relu", 64, 64), "tile-k=16")
     assert err.endswith("error: tforge-gpu-tile: tile-k needs a matmul")
