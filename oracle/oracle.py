@@ -19,7 +19,9 @@ Contents, each a restatement of the reference (paths in the TensorForge tree):
   matmul_fma / matmul_nofma / epilogue   C closed forms in tforge_oracle.c;
       pinned bit-for-bit by the e1 bitwise-difference counts.
   e1_metrics(out, ref, bound)            bench/e1_numerics.py:93-104
-  mbr_vec6x16 / time_*                   the CPU baseline port (tforge_oracle.c).
+  mbr_vec6x16 / matmul_scalar_mnk / time_*   the CPU baseline port and the default
+      scalar pipeline's loop (tforge_oracle.c); pinned by the err/bound the reference's
+      CPU results hold for both (results/cpu/stage4.csv, stage6_best.csv).
 
 Nothing here is "parity unpinned": every function above has a known-answer
 test against files the reference itself holds (tests/test_oracle_golden.py).

@@ -12,6 +12,12 @@ small JSON fixtures next to this script:
                           results/gpu/stage8.csv and stage7.csv (identical for
                           every TF variant of a shape, since they are bitwise
                           equal), per workload x shape.
+  cpu_err_bound.json      the err/bound of the reference's CPU pipelines in
+                          results/cpu/stage4.csv and stage6_best.csv per
+                          workload x shape: the default scalar pipeline
+                          (params baseline / scalar-baseline, no FMA, m-n-k
+                          loops) and the reg-tile=6,16,4 AVX2 FMA kernel
+                          (params vec-r6x16x4).
   stage9_costmodel.json   every 4th row of results/gpu/stage9_autotune.csv and
                           e2_a6000_autotune.csv reduced to the cost model's
                           inputs (config, padded shape, blocks/SM) and outputs
@@ -62,6 +68,22 @@ def err_bound(ref):
     return out
 
 
+def cpu_err_bound(ref):
+    out = {}
+    forms = {"baseline": "scalar", "scalar-baseline": "scalar", "vec-r6x16x4": "vec6x16"}
+    for name in ("stage4.csv", "stage6_best.csv"):
+        for r in csv.DictReader(open(ref / "results/cpu" / name)):
+            form = forms.get(r["params"])
+            if r["workload"] not in ("matmul", "mbr") or form is None:
+                continue
+            val = re.search(r"err/bound=([0-9.e+-]+)", r["correctness"]).group(1)
+            entry = out.setdefault(f"{r['workload']}/{r['shape']}", {})
+            if form in entry and entry[form]["err_over_bound"] != val:
+                raise SystemExit(f"CPU rows disagree at {r['workload']}/{r['shape']} {form}")
+            entry[form] = {"err_over_bound": val, "source": f"results/cpu/{name} params={r['params']}"}
+    return out
+
+
 def costmodel(ref):
     rows = []
     for name, sms, bw in (("stage9_autotune.csv", 188, 1530e9), ("e2_a6000_autotune.csv", 84, 768e9)):
@@ -86,6 +108,7 @@ def main():
     ref = pathlib.Path(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
     (HERE / "e1_known_answers.json").write_text(json.dumps(e1(ref), indent=1, sort_keys=True) + "\n")
     (HERE / "stage8_err_bound.json").write_text(json.dumps(err_bound(ref), indent=1, sort_keys=True) + "\n")
+    (HERE / "cpu_err_bound.json").write_text(json.dumps(cpu_err_bound(ref), indent=1, sort_keys=True) + "\n")
     rows = costmodel(ref)[::4]  # every 4th row keeps the fixture small; all shapes stay covered
     keys = list(rows[0])
     (HERE / "stage9_costmodel.json").write_text(

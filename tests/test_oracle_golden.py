@@ -21,6 +21,7 @@ from oracle import oracle as o
 GOLDEN = pathlib.Path(__file__).resolve().parent / "golden"
 E1 = json.loads((GOLDEN / "e1_known_answers.json").read_text())
 STAGE8 = json.loads((GOLDEN / "stage8_err_bound.json").read_text())
+CPU = json.loads((GOLDEN / "cpu_err_bound.json").read_text())
 
 _cache = {}
 
@@ -73,6 +74,27 @@ def test_stage8_err_over_bound(key):
     want = STAGE8[key]["err_over_bound"]
     digits = len(want.replace(".", "").split("e")[0].lstrip("0"))
     assert sig(o.e1_metrics(out, ref, bound)["max_err_over_bound"], digits) == float(want)
+
+
+@pytest.mark.parametrize("key", sorted(CPU))
+def test_cpu_pipeline_err_over_bound(key):
+    """results/cpu/stage4.csv, stage6_best.csv: the reference's default scalar
+    CPU pipeline (m-n-k loops, no FMA) and its reg-tile=6,16,4 AVX2 FMA kernel
+    at ten shapes, ragged ones included; the oracle's scalar loop and its
+    6x16x4 port give the same err/bound to the printed digits."""
+    wl, m, n, k = shape_of(key)
+    ins = o.make_inputs(wl, m, n, k)
+    ref, bound = o.fp64_reference(wl, ins)
+    mbr = wl == "mbr"
+    outs = {"scalar": o.matmul_scalar_mnk(ins["a"], ins["b"]),
+            "vec6x16": o.mbr_vec6x16(ins["a"], ins["b"], ins["bias"] if mbr else None, relu=mbr)}
+    if mbr:
+        outs["scalar"] = o.epilogue(outs["scalar"], ins["bias"], relu=True)
+    for form, want in CPU[key].items():
+        val = want["err_over_bound"]
+        digits = len(val.replace(".", "").split("e")[0].lstrip("0"))
+        got = o.e1_metrics(outs[form], ref, bound)["max_err_over_bound"]
+        assert sig(got, digits) == float(val), (key, form, got, val)
 
 
 @pytest.mark.parametrize("shape", [(256, 256, 256), (127, 129, 65), (777, 1111, 333), (6, 16, 4), (5, 15, 3)])
