@@ -107,6 +107,12 @@ def cpu_baseline(target_s=12.0):
     reps = max(1, min(50, int(target_s / max(first_ns * 1e-9, 1e-3))))
     med_ns = o.time_vec6x16(a, b, bias, 0, reps)
     vec_gflops = flops / med_ns
+    # The same port at 512^3, the largest shape the reference measured its CPU
+    # kernel at (results/cpu/stage6_best.csv: 87.8 GFLOP/s on one Zen 2 core);
+    # at 2048^3 its loops stream B from memory for every 6-row strip.
+    s = 512
+    ns512 = o.time_vec6x16(a[:s, :s].copy(), b[:s, :s].copy(), bias[:s].copy(), 2, 20)
+    gflops_512 = 2.0 * s ** 3 / ns512
     # scalar default pipeline on a row slice (its cost is linear in rows)
     rows = 64
     sc_ns = o.time_scalar(a[:rows], b, bias, 0, 1)
@@ -137,7 +143,7 @@ def cpu_baseline(target_s=12.0):
     return {"value": vec_gflops / 1e3, "unit": "TFLOP/s", "cores": 1, "kind": "port",
             "sample": (f"full 2048^3 fused mbr, oracle 6x16x4 AVX2-FMA port of the reference's best CPU "
                        f"pipeline (reg-tile=6,16,4 vectorize=1), 1 thread, median of {reps} reps"),
-            "gflops": vec_gflops, "host_cpu": cpu, "avx2": bool(o.lib().tfo_have_avx2()),
+            "gflops": vec_gflops, "gflops_at_512": gflops_512, "host_cpu": cpu, "avx2": bool(o.lib().tfo_have_avx2()),
             "scalar_default_pipeline_gflops": sc_gflops, "scalar_sample": f"{rows} of {M} rows",
             "numpy_1thread_gflops": np_gflops, "seconds": time.perf_counter() - t0}
 
