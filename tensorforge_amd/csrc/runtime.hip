@@ -169,7 +169,9 @@ int select_launches(tf_kernel *k) {
                                                     " threads per block exceeds 1024"));
     L.block = dim3((unsigned)tx, (unsigned)ty, 1);
     L.grid = dim3((unsigned)std::max(1L, ceil_div(st.N, o.bn)), (unsigned)std::max(1L, ceil_div(st.M, o.bm)), 1);
-    if (o.split_k > 1) {
+    // split-k splits the K loop of GEMM stages; the element-op launches of an
+    // unfused program run as they are.  Without tile-k it is an error.
+    if (o.split_k > 1 && (gemm || o.tile_k == 0)) {
       if (!staged)
         return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc,
                                                   "tforge-gpu-pipeline: split-k needs tile-k"));

@@ -214,6 +214,9 @@ def test_split_k_geometry_and_errors():
     assert compile_err(prog, "split-k=2").endswith("error: tforge-gpu-pipeline: split-k needs tile-k")
     for bad in ("split-k=0", "split-k=65", "split-k=x"):
         assert "invalid value" in compile_err(prog, staged + " " + bad)
+    # unfused program: split-k applies to the matmul launch; bias_add and relu run as they are
+    unf = _lib.Kernel(tc.gen_mlir("mbr", 128, 128, 256), staged + " split-k=4 fuse-elementwise=0").launches()
+    assert [(l["ops"], l["grid"][2]) for l in unf] == [("matmul", 4), ("bias_add", 1), ("relu", 1)]
 
 
 def test_mask_edges_accepts_any_shape():

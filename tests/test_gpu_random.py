@@ -7,7 +7,15 @@ for configurations that have a masked twin).  Every draw meets the reference's
 bar: no NaN in the NaN-prefilled output, max err/bound <= 1 against the FP64
 reference (python/tforge_gpu.py:134-145), exact ReLU masks.  A masked draw
 also equals the pad path (zero-padded copies through the unmasked kernel,
-the reference runner's method) bit for bit.
+the reference runner's method) bit for bit, and a masked mbr draw run unfused
+(fuse-elementwise=0: the matmul, bias_add and relu as three launches) equals
+the fused kernel bit for bit (the fused epilogue performs the same IEEE
+operations in registers).
+
+Two more families: 32 element-op programs (relu, bias_add, add; shapes up to
+3000 x 3000; every thread tile 1..8 x 1..8 that compiles) bit-exact against
+NumPy float32 (python/tforge_gpu.py:116-126), and 16 residual blocks at ragged
+shapes with masked tiles against the two-layer composed bound.
 """
 
 import numpy as np
@@ -17,6 +25,7 @@ from oracle import oracle as o
 from tensorforge_amd import _lib
 from tensorforge_amd import costmodel as cm
 from tensorforge_amd import tforge_cpu as tc
+from tensorforge_amd import tforge_gpu as tg
 
 pytestmark = pytest.mark.gpu
 
@@ -42,7 +51,37 @@ def _draws(count=48, seed=2026):
     return out
 
 
+def _elt_draws(count=32, seed=2027):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        wl = ("relu", "bias_add", "add")[rng.integers(3)]
+        m, n = (int(v) for v in rng.integers(1, 3001, size=2))
+        tm, tn = (int(v) for v in rng.choice([1, 2, 4, 8], size=2))
+        bm, bn = tm * int(rng.choice([1, 2, 4, 8, 16])), tn * int(rng.choice([4, 8, 16, 32, 64]))
+        opts = f"block-tile={bm},{bn} thread-tile={tm},{tn}"
+        try:
+            _lib.Kernel(tc.gen_mlir(wl, m, n, None), opts, "t.mlir")
+        except RuntimeError:
+            continue  # e.g. not a whole number of waves: tf_compile refuses it
+        out.append((wl, (m, n), opts))
+    return out
+
+
+def _resmlp_draws(count=16, seed=2028):
+    rng = np.random.default_rng(seed)
+    space = [tuple(e["cfg"][:5]) for e in _lib.registry() if e["family"] == "staged" and e["name"].endswith("_masked")
+             and e["cfg"][5] == 1 and e["cfg"][6] == 1]
+    out = []
+    while len(out) < count:
+        m, n, k = (int(v) for v in rng.integers(1, 301, size=3))
+        out.append(((m, n, k), space[rng.integers(len(space))]))
+    return out
+
+
 DRAWS = _draws()
+ELT_DRAWS = _elt_draws()
+RESMLP_DRAWS = _resmlp_draws()
 
 
 def _run(workload, m, n, k, options, ins, logical=None):
@@ -71,3 +110,29 @@ def test_random_draw(workload, shape, cfg, split, masked):
         if workload == "mbr":
             assert o.mask_mismatches(out, o.preactivation64(ins), bound) == 0
         assert o.bitwise_diff(out, padded) == 0
+    if workload == "mbr" and masked:  # the pad path takes single-launch programs only
+        unfused = _run(workload, m, n, k, opts + " mask-edges=1 fuse-elementwise=0", ins)
+        assert o.bitwise_diff(unfused, padded) == 0
+
+
+@pytest.mark.parametrize("workload,shape,opts", ELT_DRAWS,
+                         ids=[f"{d[0]}-{d[1][0]}x{d[1][1]}-{d[2].replace(' ', '-')}" for d in ELT_DRAWS])
+def test_random_element_op(workload, shape, opts):
+    m, n = shape
+    print(f"draw {workload} {shape} {opts}", flush=True)
+    d, launch = tg.compile_kernel(workload, m, n, None, opts, tag="test")
+    res, _ = tg.check(workload, m, n, None, d, launch)
+    assert res["pass"], res
+
+
+@pytest.mark.parametrize("shape,cfg", RESMLP_DRAWS,
+                         ids=[f"{'x'.join(map(str, d[0]))}-b{d[1][0]}x{d[1][1]}-t{d[1][2]}x{d[1][3]}-k{d[1][4]}"
+                              for d in RESMLP_DRAWS])
+def test_random_residual_block(shape, cfg):
+    m, n, k = shape
+    print(f"draw resmlp {shape} {cfg}", flush=True)
+    ins = tc.make_inputs("resmlp", m, n, k)
+    kern = _lib.Kernel(tc.gen_mlir("resmlp", m, n, k), STAGED.format(*cfg) + " mask-edges=1", "t.mlir")
+    y = np.empty((m, n), np.float32)
+    kern.run([np.ascontiguousarray(v) for v in ins.values()], y)
+    assert tg._resmlp_check(ins, y)["pass"]
