@@ -12,6 +12,11 @@ the reference runner's method) bit for bit, and a masked mbr draw run unfused
 the fused kernel bit for bit (the fused epilogue performs the same IEEE
 operations in registers).
 
+A third GEMM family draws 24 cases from the promote=0 / vectorize=0
+instantiations (the ablation rungs, masked twins included) and from
+promote=1 vectorize=1 ones with xcd-swizzle=0, at random shapes up to 400 and
+split factors up to 3.
+
 Two more families: 32 element-op programs (relu, bias_add, add; shapes up to
 3000 x 3000; every thread tile 1..8 x 1..8 that compiles) bit-exact against
 NumPy float32 (python/tforge_gpu.py:116-126), and 16 residual blocks at ragged
@@ -79,7 +84,32 @@ def _resmlp_draws(count=16, seed=2028):
     return out
 
 
+def _variant_draws(count=24, seed=2029):
+    """The promote=0 / vectorize=0 instantiations (the ablation rungs) and
+    promote=1 vectorize=1 ones with the XCD tile order switched off."""
+    rng = np.random.default_rng(seed)
+    reg = [e for e in _lib.registry() if e["family"] == "staged"]
+    rungs = [e for e in reg if (e["cfg"][5], e["cfg"][6]) != (1, 1)]
+    plain = [e for e in reg if (e["cfg"][5], e["cfg"][6]) == (1, 1) and not e["name"].endswith("_masked")]
+    out = []
+    while len(out) < count:
+        e = rungs[rng.integers(len(rungs))] if rng.random() < 0.7 else plain[rng.integers(len(plain))]
+        bm, bn, tm, tn, bk, pr, vec = e["cfg"]
+        masked = e["name"].endswith("_masked")
+        m, n, k = (int(v) for v in rng.integers(1, 401, size=3))
+        opts = f"block-tile={bm},{bn} thread-tile={tm},{tn} tile-k={bk} promote={pr} vectorize={vec}"
+        kk = k if masked else cm.padded((bm, bn, tm, tn, bk), m, n, k)[2]
+        split = int(rng.choice([1, 1, 2, 3]))
+        if split > 1 and -(-kk // bk) >= split:
+            opts += f" split-k={split}"
+        if (pr, vec) == (1, 1) or rng.random() < 0.5:
+            opts += " xcd-swizzle=0"
+        out.append((("mbr", "matmul")[rng.integers(2)], (m, n, k), (bm, bn, tm, tn, bk), opts, masked))
+    return out
+
+
 DRAWS = _draws()
+VARIANT_DRAWS = _variant_draws()
 ELT_DRAWS = _elt_draws()
 RESMLP_DRAWS = _resmlp_draws()
 
@@ -113,6 +143,24 @@ def test_random_draw(workload, shape, cfg, split, masked):
     if workload == "mbr" and masked:  # the pad path takes single-launch programs only
         unfused = _run(workload, m, n, k, opts + " mask-edges=1 fuse-elementwise=0", ins)
         assert o.bitwise_diff(unfused, padded) == 0
+
+
+@pytest.mark.parametrize("workload,shape,cfg,opts,masked", VARIANT_DRAWS,
+                         ids=[f"{d[0]}-{'x'.join(map(str, d[1]))}-{d[3].replace(' ', '-')}{'-masked' if d[4] else ''}"
+                              for d in VARIANT_DRAWS])
+def test_random_variant(workload, shape, cfg, opts, masked):
+    m, n, k = shape
+    ins = o.make_inputs(workload, m, n, k)
+    print(f"draw {workload} {shape} {opts} masked={masked}", flush=True)
+    padded = _run(workload, m, n, k, opts, ins, logical=cm.padded(cfg, m, n, k))
+    outs = [padded, _run(workload, m, n, k, opts + " mask-edges=1", ins)] if masked else [padded]
+    ref, bound = o.fp64_reference(workload, ins)
+    for out in outs:
+        assert not np.isnan(out).any()
+        assert o.e1_metrics(out, ref, bound)["max_err_over_bound"] <= 1.0
+        if workload == "mbr":
+            assert o.mask_mismatches(out, o.preactivation64(ins), bound) == 0
+        assert o.bitwise_diff(out, padded) == 0
 
 
 @pytest.mark.parametrize("workload,shape,opts", ELT_DRAWS,
