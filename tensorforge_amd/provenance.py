@@ -1,17 +1,27 @@
 """Provenance fields shared by every results CSV row (python/provenance.py:1-70).
 
 The column set is unchanged so CSVs stay comparable with the reference's.  On
-this backend "mlir_llvm_version" holds the LLVM version of hipcc (there is no
+this backend "mlir_llvm_version" holds the version of ROCm's LLVM (there is no
 MLIR in the tool chain) and "cuda_version" holds the HIP version.
+
+Everything is read from files (the git refs, the ROCm headers, /proc/cpuinfo)
+rather than from tools run in a shell: these rows are written from processes
+that hold the GPU, sometimes under a profiler whose preloaded library sets up
+the GPU in every child, and a tool that replaces itself with another program
+(exec) from such a process is not allowed.  The commit therefore carries no
+"-dirty" mark.
 """
 
 import csv
 import datetime
 import os
 import pathlib
+import re
+import socket
 import subprocess
 
 ROOT = pathlib.Path(__file__).resolve().parent.parent
+ROCM = pathlib.Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
 FIELDS = [
     "commit", "mlir_llvm_version", "cuda_version", "device", "job_id", "date",
@@ -21,22 +31,39 @@ FIELDS = [
 ]
 
 
-def _sh(cmd):
+def _read(path):
     try:
-        return subprocess.run(cmd, shell=True, capture_output=True, text=True, timeout=60).stdout.strip()
-    except (OSError, subprocess.SubprocessError):
+        return pathlib.Path(path).read_text()
+    except OSError:
         return ""
 
 
+def _commit():
+    """Short hash of HEAD from .git (empty where the tree has no .git)."""
+    git = ROOT / ".git"
+    head = _read(git / "HEAD").strip()
+    if not head.startswith("ref: "):
+        return head[:7]
+    name = head[5:]
+    sha = _read(git / name).strip()
+    if not sha:
+        for line in _read(git / "packed-refs").splitlines():
+            if line.endswith(" " + name):
+                sha = line.split()[0]
+    return sha[:7]
+
+
+def _define(text, name):
+    m = re.search(rf"#define\s+{name}\s+\"?([^\s\"]+)", text)
+    return m.group(1) if m else ""
+
+
 def common():
-    dirty = _sh(f"git -C {ROOT} status --porcelain --untracked-files=no")
-    commit = _sh(f"git -C {ROOT} rev-parse --short HEAD") + ("-dirty" if dirty else "")
-    llvm = _sh("/opt/rocm/bin/hipcc --version 2>/dev/null | grep -o 'clang version [0-9.a-z]*'").replace(
-        "clang version ", "")
-    hip = _sh("/opt/rocm/bin/hipcc --version 2>/dev/null | grep -o 'HIP version: [0-9.]*'").replace(
-        "HIP version: ", "")
+    hipv = _read(ROCM / "include/hip/hip_version.h")
+    hip = ".".join(_define(hipv, f"HIP_VERSION_{p}") for p in ("MAJOR", "MINOR", "PATCH")).strip(".")
+    llvm = _define(_read(ROCM / "lib/llvm/include/flang/Version.inc"), "FLANG_VERSION_STRING")
     return {
-        "commit": commit,
+        "commit": _commit(),
         "mlir_llvm_version": llvm,
         "cuda_version": hip,
         "job_id": os.environ.get("SLURM_JOB_ID", os.environ.get("GRAFT_JOB_ID", "none")),
@@ -45,15 +72,23 @@ def common():
 
 
 def cpu_model():
-    return _sh("lscpu | grep -m1 'Model name' | sed 's/Model name:[ ]*//'")
+    for line in _read("/proc/cpuinfo").splitlines():
+        if line.startswith("model name"):
+            return line.split(":", 1)[1].strip()
+    return ""
 
 
 def save_lscpu(outdir):
+    """hostname and lscpu's report (lscpu run directly as a child process)."""
     outdir = pathlib.Path(outdir)
     outdir.mkdir(parents=True, exist_ok=True)
     job = os.environ.get("SLURM_JOB_ID", "none")
     p = outdir / f"lscpu_{job}.txt"
-    p.write_text(_sh("hostname") + "\n" + _sh("lscpu") + "\n")
+    try:
+        report = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=60).stdout
+    except (OSError, subprocess.SubprocessError):
+        report = ""
+    p.write_text(socket.gethostname() + "\n" + report + "\n")
     return p
 
 
