@@ -27,7 +27,10 @@
 //    middle of slab t+2), so the LDS writes do not wait on HBM latency under
 //    full-chip load (one set, 1.5 slabs ahead, for the register-heavy
 //    configurations); the slab loop is unrolled by two so buffer and set
-//    indices are compile-time.  The barrier sits before the slab's last
+//    indices are compile-time.  (The loads are conditional near the end of
+//    K, so the compiler's wait before every other slab's stores covers both
+//    sets; loads issued a slab earlier have landed by then, and clamped
+//    unconditional loads with exact waits measured no faster.)  The barrier sits before the slab's last
 //    chunk so those MFMAs hide the next slab's first LDS reads.  Each
 //    chunk's MFMAs are scheduled around the next chunk's fragment reads in a
 //    measured order.  Row padding makes the b128 fragment reads and the b32
