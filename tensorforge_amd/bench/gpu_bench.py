@@ -59,7 +59,12 @@ def main(argv=None):
     variants = [v.split("=", 1) for v in args.variant]
     shapes = SHAPES
     if args.shapes:
+        # MxNxK, or MxN for element-op workloads (K = 0, as the CSV rows write it)
         shapes = [tuple(int(x) for x in s.split("x")) for s in args.shapes.split(",")]
+        bad = [s for s in shapes if len(s) not in (2, 3)]
+        if bad:
+            ap.error(f"--shapes takes MxNxK or MxN, got {args.shapes}")
+        shapes = [s if len(s) == 3 else s + (0,) for s in shapes]
     base = provenance.common()
     out = None if args.check_only else provenance.CsvWriter(args.csv)
     failures = 0
