@@ -13,7 +13,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float relu_ieee(float x) { return (x > 0.0f || x != x) ? x : 0.0f; }
 
 // Applies the epilogue ops first.. to four consecutive outputs C[m, n..n+3]
-// (first = 1 when the caller has already added a prefetched bias).
+// (first = 1 when the caller has already added a prefetched bias).  STREAM:
+// the add operand is read once by this launch, so its load is non-temporal
+// (the element-op kernels); the bias, reused by every row, stays cached.
+template <bool STREAM = false>
 __device__ __forceinline__ f32x4 apply_epi4(f32x4 v, const EpiParams &e, long m, int n, int first = 0) {
 #pragma unroll
   for (int i = 0; i < kMaxEpi; ++i) {
@@ -28,7 +31,8 @@ __device__ __forceinline__ f32x4 apply_epi4(f32x4 v, const EpiParams &e, long m,
       v.z = relu_ieee(v.z);
       v.w = relu_ieee(v.w);
     } else if (kind == EPI_ADD) {
-      v += *reinterpret_cast<const f32x4 *>(e.ptr[i] + m * e.ldr[i] + n);
+      const f32x4 *r = reinterpret_cast<const f32x4 *>(e.ptr[i] + m * e.ldr[i] + n);
+      v += STREAM ? __builtin_nontemporal_load(r) : *r;
     } else if (kind == EPI_ADD_SELF) {
       v = v + v;
     }
