@@ -18,7 +18,7 @@ promote=1 vectorize=1 ones with xcd-swizzle=0, at random shapes up to 400 and
 split factors up to 3.
 
 Two more families: 32 element-op programs (relu, bias_add, add; shapes up to
-3000 x 3000; every thread tile 1..8 x 1..8 that compiles) bit-exact against
+3000 x 8192, half of them with rows of whole workgroup chunks; every thread tile 1..8 x 1..8 that compiles) bit-exact against
 NumPy float32 (python/tforge_gpu.py:116-126), and 16 residual blocks at ragged
 shapes with masked tiles against the two-layer composed bound.
 """
@@ -65,6 +65,8 @@ def _elt_draws(count=32, seed=2027):
         tm, tn = (int(v) for v in rng.choice([1, 2, 4, 8], size=2))
         bm, bn = tm * int(rng.choice([1, 2, 4, 8, 16])), tn * int(rng.choice([4, 8, 16, 32, 64]))
         opts = f"block-tile={bm},{bn} thread-tile={tm},{tn}"
+        if rng.random() < 0.5 and bm * bn <= 4096:  # rows of whole workgroup chunks
+            n = bm * bn * int(rng.integers(1, max(2, 8192 // (bm * bn) + 1)))
         try:
             _lib.Kernel(tc.gen_mlir(wl, m, n, None), opts, "t.mlir")
         except RuntimeError:
