@@ -61,7 +61,15 @@ __global__ void elementwise_kernel(EltParams p) {
     // 6.80 against 6.38 TB/s for relu at 16384^2 with cached accesses).
     if (p.vec_ok && n_base + TN <= p.N) {
       // All loads first (rows past M read row M-1 and are not stored), so
-      // they are in flight together; then the ops and the stores.
+      // they are in flight together; then the ops and the stores.  A chain
+      // that starts with bias_add loads its bias here too (cached: every row
+      // reads it), rather than behind the epilogue's per-op branch, where
+      // each thread would wait for X before asking for the bias.
+      const bool pre_bias = p.epi.nops > 0 && p.epi.kind[0] == EPI_BIAS;
+      f32x4 bv[TN / 4];
+#pragma unroll
+      for (int j = 0; j < TN / 4; ++j)
+        bv[j] = pre_bias ? *reinterpret_cast<const f32x4 *>(p.epi.ptr[0] + n_base + 4 * j) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       f32x4 x[TM][TN / 4];
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
@@ -77,8 +85,9 @@ __global__ void elementwise_kernel(EltParams p) {
 #pragma unroll
         for (int j = 0; j < TN / 4; ++j) {
           const int n = (int)n_base + 4 * j;
-          __builtin_nontemporal_store(apply_epi4<true>(x[i][j], p.epi, m, n),
-                                      reinterpret_cast<f32x4 *>(p.Y + m * p.ldy + n));
+          const f32x4 v = pre_bias ? apply_epi4<true>(x[i][j] + bv[j], p.epi, m, n, 1)
+                                   : apply_epi4<true>(x[i][j], p.epi, m, n);
+          __builtin_nontemporal_store(v, reinterpret_cast<f32x4 *>(p.Y + m * p.ldy + n));
         }
       }
       return;
