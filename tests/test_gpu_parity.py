@@ -148,6 +148,38 @@ def test_elementwise_row_chunks_bit_exact(workload, opts, shape):
     assert res["pass"], res
 
 
+@pytest.mark.parametrize("workload", ["relu", "bias_add", "add"])
+def test_elementwise_misaligned_buffers(workload):
+    """tf_launch on buffers 4 bytes past a 16-byte boundary (torch views one
+    float into an allocation): the element-op kernel drops to its 32-bit path
+    (and loads the bias in the epilogue) and stays bit-exact; N = 1024 would
+    otherwise take the 128-bit path."""
+    import torch
+    dev = torch.device("cuda:0")
+    m, n = 37, 1024
+    opts = "block-tile=4,256 thread-tile=1,4"
+    ins = o.make_inputs(workload, m, n, None)
+    views = []
+    for v in ins.values():
+        flat = np.ascontiguousarray(v).ravel()
+        base = torch.zeros(flat.size + 1, device=dev)
+        base[1:] = torch.from_numpy(flat).to(dev)
+        views.append(base[1:].view(v.shape))
+    out_base = torch.full((m * n + 1,), float("nan"), device=dev)
+    out = out_base[1:].view(m, n)
+    assert all(t.data_ptr() % 16 == 4 for t in views + [out])
+    kern = _lib.Kernel(tc.gen_mlir(workload, m, n, None), opts, "t.mlir")
+    kern.launch([t.data_ptr() for t in views] + [out.data_ptr()], torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    a = ins["a"]
+    with np.errstate(invalid="ignore"):
+        want = {"relu": lambda: np.where(np.isnan(a) | (a > 0), a, np.float32(0.0)),
+                "bias_add": lambda: a + ins["bias"][None, :],
+                "add": lambda: a + ins["b"]}[workload]().astype(np.float32)
+    assert o.bitwise_diff(got, want) == 0
+
+
 def test_launch_abi_matches_run():
     """tf_launch on caller-owned device buffers (torch) gives the same bits as tf_run."""
     import torch
