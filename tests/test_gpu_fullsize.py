@@ -1,4 +1,4 @@
-"""Every BASELINE configuration at its full size, through tf_launch, with the
+"""Every benchmark configuration at its full size, through tf_launch, with the
 options the benchmarks use (autotuned, else the cost model's pick).
 
 A full FP64 reference of the largest problems costs minutes on the host, so
@@ -28,7 +28,7 @@ from tensorforge_amd import tforge_gpu as tg
 
 pytestmark = pytest.mark.gpu
 
-# examples/mbr.mlir, the 2048^3 headline, plain matmul
+# The benchmark configurations: examples/mbr.mlir, the 2048^3 headline, plain matmul
 # 512..8192^3, the rectangular MLP layers (skinny and short-K included).
 CASES = [("mbr", 256, 256, 128), ("mbr", 2048, 2048, 2048),
          ("matmul", 512, 512, 512), ("matmul", 1024, 1024, 1024), ("matmul", 2048, 2048, 2048),
@@ -85,7 +85,7 @@ def test_full_size_properties(workload, m, n, k):
 
 
 def test_full_size_residual_block():
-    """The residual block at its BASELINE size (x 4096x2048, W1 2048x8192,
+    """The residual block at its benchmark size (x 4096x2048, W1 2048x8192,
     W2 8192x2048) with the measured best tiles."""
     torch, dev = _torch()
     m, n, k = 4096, 2048, 8192

@@ -1,6 +1,6 @@
 """GPU parity: libtforge_hip's kernels on cuda:0 against the CPU oracle.
 
-Bars (python/tforge_gpu.py:112-145):
+Bars (python/tforge_gpu.py:112-145, plus exact ReLU masks):
   * staged MFMA kernels: err/bound <= 1 against the FP64 reference with the
     reference's gamma_{K+1} bound, no NaN (outputs are NaN-prefilled), and
     exact ReLU masks wherever |pre-activation| exceeds the bound;
