@@ -133,15 +133,15 @@ def test_elementwise_bit_exact(workload, shape, opts):
 
 @pytest.mark.parametrize("workload", ["relu", "bias_add", "add"])
 @pytest.mark.parametrize("opts,shape", [
-    ("block-tile=16,16 thread-tile=1,1", (37, 512)),     # the reference default: 256-element chunks, scalar
-    ("block-tile=16,16 thread-tile=2,2", (20, 1024)),    # 4 elements per thread: float4 chunks
-    ("block-tile=4,256 thread-tile=1,4", (5, 2048)),     # 1024-element chunks
-    ("block-tile=8,512 thread-tile=2,8", (9, 4096)),     # 4096-element chunks, 4 vectors per thread
+    ("block-tile=16,16 thread-tile=1,1", (37, 512)),     # the reference default, 32-bit path
+    ("block-tile=16,16 thread-tile=2,2", (20, 1024)),    # 2 x 2 per thread, 32-bit path
+    ("block-tile=4,256 thread-tile=1,4", (5, 2048)),     # one 128-bit vector per thread
+    ("block-tile=8,512 thread-tile=2,8", (9, 4096)),     # 4 vectors per thread
 ])
 def test_elementwise_row_chunks_bit_exact(workload, opts, shape):
-    """Rows that are whole multiples of a workgroup's BM*BN elements, M not a
-    multiple of the block tile (the grid's last row of workgroups is partly
-    past M), scalar and 128-bit paths, 1 to 4 vectors per thread."""
+    """N a multiple of a workgroup's BM*BN elements and M not a multiple of
+    the block tile (the grid's last row of workgroups is partly past M), on
+    the 32-bit and 128-bit paths, 1 to 4 vectors per thread."""
     m, n = shape
     d, launch = tg.compile_kernel(workload, m, n, None, opts, tag="test")
     res, out = tg.check(workload, m, n, None, d, launch)
