@@ -7,6 +7,8 @@ no fallback: every call on the hot path goes through the gfx950 kernels.
 import ctypes
 import pathlib
 
+import numpy as np
+
 PKG = pathlib.Path(__file__).resolve().parent
 LIB_PATH = PKG / "libtforge_hip.so"
 
@@ -145,7 +147,36 @@ class Kernel:
                 "blocks_per_sm": r.blocks_per_cu, "theo_occupancy": round(r.theo_occupancy, 3),
                 "threads": r.threads}
 
+    def _expect_sizes(self, logical):
+        """Element count of each buffer (inputs, then the output) that tf_run
+        reads or writes: the compiled shapes, or for a logical (unpadded) run
+        of a single-matmul program A (M x K), B (K x N), bias (N), C (M x N)."""
+        bufs = self.buffers()
+        if logical is None:
+            return [int(b["shape"][0]) * int(b["shape"][1]) for b in bufs]
+        if len(self.launches()) != 1 or len(bufs) not in (3, 4):
+            return None  # tf_run refuses logical sizes here with its own message
+        m, n, k = (int(x) for x in logical)
+        return [m * k, k * n] + [n] * (len(bufs) - 3) + [m * n]
+
+    def _check_host(self, arrays, out, logical):
+        # tf_run copies whole buffers from and to these pointers: a short,
+        # strided or non-float32 array would be read or written out of bounds.
+        nargs = len(self.buffers()) - 1
+        if len(arrays) != nargs:
+            raise ValueError(f"this program takes {nargs} input arrays, got {len(arrays)}")
+        want = self._expect_sizes(logical)
+        named = [(f"input {i}", a) for i, a in enumerate(arrays)] + ([("output", out)] if out is not None else [])
+        for i, (what, a) in enumerate(named):
+            if not isinstance(a, np.ndarray) or a.dtype != np.float32 or not a.flags.c_contiguous:
+                raise TypeError(f"{what} must be a C-contiguous float32 numpy array")
+            if want is not None and a.size != want[i if what != "output" else -1]:
+                raise ValueError(f"{what} has {a.size} elements, the program needs {want[i if what != 'output' else -1]}")
+
     def launch(self, device_ptrs, stream=0):
+        nbuf = len(self.buffers())
+        if len(device_ptrs) != nbuf:
+            raise ValueError(f"this program takes {nbuf} device buffers (inputs, then the output), got {len(device_ptrs)}")
         arr = (P * len(device_ptrs))(*[P(int(p)) for p in device_ptrs])
         check(lib().tf_launch(self.h, arr, P(int(stream)) if stream else None))
 
@@ -161,12 +192,15 @@ class Kernel:
         return None if mnk is None else (LL * 3)(*[int(x) for x in mnk])
 
     def run(self, inputs, out, mode=TF_MODE_KERNEL, logical=None):
+        self._check_host(inputs, out, logical)
         check(lib().tf_run(self.h, mode, self._logical(logical), self._host_ptrs(inputs),
                            out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
         return out
 
     def bench(self, inputs=None, mode=TF_MODE_KERNEL, logical=None, seed=1234, warmup=10, reps=100, flush=False):
         r = BenchResult()
+        if inputs is not None:
+            self._check_host(inputs, None, logical)
         ptrs = self._host_ptrs(inputs) if inputs is not None else None
         check(lib().tf_bench(self.h, mode, self._logical(logical), ptrs, seed, warmup, reps, int(flush),
                              ctypes.byref(r)))

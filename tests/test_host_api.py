@@ -112,3 +112,32 @@ def test_provenance_fields_are_the_reference_schema(tmp_path):
 def test_flops_convention():
     assert tc.flops_or_bytes("mbr", 2048, 2048, 2048) == ("GFLOP/s", 2.0 * 2048 ** 3)
     assert tc.flops_or_bytes("resmlp", 4096, 2048, 8192)[1] == 4.0 * 4096 * 2048 * 8192
+
+
+def test_host_arrays_and_pointer_counts_are_validated():
+    """tf_run copies whole buffers from and to host pointers and tf_launch
+    reads one device pointer per buffer, so the Python mirror checks counts,
+    dtype, layout and element counts before calling (no GPU needed: every
+    case raises first)."""
+    import numpy as np
+    import pytest
+    from tensorforge_amd import _lib, tforge_cpu as tc
+    k = _lib.Kernel(tc.gen_mlir("mbr", 64, 32, 16), "")
+    a, b, bias, c = (np.zeros(s, np.float32) for s in ((64, 16), (16, 32), (32,), (64, 32)))
+    with pytest.raises(ValueError, match="takes 3 input arrays, got 1"):
+        k.run([a], c)
+    with pytest.raises(TypeError, match="input 2 must be a C-contiguous float32"):
+        k.run([a, b, bias.astype(np.float64)], c)
+    with pytest.raises(TypeError, match="input 1 must be a C-contiguous float32"):
+        k.run([a, np.zeros((32, 16), np.float32).T, bias], c)
+    with pytest.raises(ValueError, match="input 2 has 31 elements, the program needs 32"):
+        k.run([a, b, bias[:31]], c)
+    with pytest.raises(ValueError, match="output has 1984 elements, the program needs 2048"):
+        k.run([a, b, bias], np.zeros((64, 31), np.float32))
+    with pytest.raises(ValueError, match="takes 4 device buffers"):
+        k.launch([1, 2, 3])
+    # logical (unpadded) sizes of a padded single-matmul program: A m x k, B k x n, bias n, C m x n
+    kp = _lib.Kernel(tc.gen_mlir("mbr", 128, 64, 32), "block-tile=128,64 thread-tile=8,4 tile-k=16 promote=1")
+    with pytest.raises(ValueError, match="input 0 has 1600 elements, the program needs 1500"):
+        kp.run([np.zeros((100, 16), np.float32), np.zeros((15, 50), np.float32), np.zeros(50, np.float32)],
+               np.zeros((100, 50), np.float32), logical=(100, 50, 15))
