@@ -137,7 +137,9 @@ int tf_kernel_info(const tf_kernel_t *k, int launch, tf_kernel_resources_t *out)
 
 /* Kernel ABI: enqueue every launch of the program on `stream` (a hipStream_t,
  * NULL for the default stream) with caller-owned device buffers in argN order,
- * shaped as compiled.  Intermediates of multi-launch programs and the split-K
+ * shaped as compiled: tf_kernel_num_buffers(k) pointers, the inputs then the
+ * result, each to the float32 elements tf_kernel_buffer_info reports.
+ * Intermediates of multi-launch programs and the split-K
  * partial-sum workspace are allocated once per handle on first use; calls on
  * one handle that overlap on different streams share them.  No
  * synchronisation.  Replaces cuLaunchKernel with the marshalled argN list
@@ -150,7 +152,10 @@ int tf_launch(tf_kernel_t *k, void *const *device_buffers, void *stream);
  * single-matmul program compiled at a padded shape: inputs and output are then
  * at the logical shape and the library pads and unpads with device copies,
  * as the reference runner does (runners/gpu/tforge-gpu-bench.cu:214-232,
- * 292-302, 323-331).  mode is TF_MODE_KERNEL or TF_MODE_BLAS. */
+ * 292-302, 323-331).  host_inputs holds one row-major float32 array per
+ * input (M x K, K x N and N elements for A, B and bias at a logical shape;
+ * the compiled shapes otherwise) and host_out has room for the result; the
+ * library copies exactly those sizes.  mode is TF_MODE_KERNEL or TF_MODE_BLAS. */
 int tf_run(tf_kernel_t *k, int mode, const long long *logical_mnk, const float *const *host_inputs,
            float *host_out);
 
