@@ -131,6 +131,16 @@ int tf_kernel_num_launches(const tf_kernel_t *k);
 int tf_kernel_launch_info(const tf_kernel_t *k, int launch, tf_launch_info_t *out);
 int tf_kernel_num_buffers(const tf_kernel_t *k); /* entry arguments + 1 result */
 int tf_kernel_buffer_info(const tf_kernel_t *k, int index, tf_buffer_info_t *out);
+/* Shape (rows x cols) of buffer `index` as tf_run / tf_bench copy it from and
+ * to host memory: the compiled shape, or, with `logical_mnk`, the logical
+ * shape of the buffer's role in the single matmul chain (A m x k, B k x n,
+ * bias 1 x n, residual and result m x n; an unused argument keeps its compiled
+ * shape).  Fails with TF_E_ARG where tf_run would refuse the logical sizes (a
+ * multi-launch program, sizes above the compiled ones, or one buffer in two
+ * roles whose logical shapes differ).  The counterpart of the reference
+ * runner's per-buffer --in-dir file sizes (runners/gpu/tforge-gpu-bench.cu:214-232). */
+int tf_kernel_host_shape(const tf_kernel_t *k, const long long *logical_mnk, int index, long long *rows,
+                         long long *cols);
 /* Resources and occupancy of one launch: the runner's --info-only
  * (runners/gpu/tforge-gpu-bench.cu:278-291). */
 int tf_kernel_info(const tf_kernel_t *k, int launch, tf_kernel_resources_t *out);
@@ -138,7 +148,8 @@ int tf_kernel_info(const tf_kernel_t *k, int launch, tf_kernel_resources_t *out)
 /* Kernel ABI: enqueue every launch of the program on `stream` (a hipStream_t,
  * NULL for the default stream) with caller-owned device buffers in argN order,
  * shaped as compiled: tf_kernel_num_buffers(k) pointers, the inputs then the
- * result, each to the float32 elements tf_kernel_buffer_info reports.
+ * result, each to the float32 elements tf_kernel_buffer_info reports.  A NULL
+ * pointer for a non-empty buffer is refused (TF_E_ARG) before any launch.
  * Intermediates of multi-launch programs and the split-K
  * partial-sum workspace are allocated once per handle on first use; calls on
  * one handle that overlap on different streams share them.  No
@@ -153,9 +164,10 @@ int tf_launch(tf_kernel_t *k, void *const *device_buffers, void *stream);
  * at the logical shape and the library pads and unpads with device copies,
  * as the reference runner does (runners/gpu/tforge-gpu-bench.cu:214-232,
  * 292-302, 323-331).  host_inputs holds one row-major float32 array per
- * input (M x K, K x N and N elements for A, B and bias at a logical shape;
- * the compiled shapes otherwise) and host_out has room for the result; the
- * library copies exactly those sizes.  mode is TF_MODE_KERNEL or TF_MODE_BLAS. */
+ * input, each of the size tf_kernel_host_shape reports for the same
+ * `logical_mnk` (M x K, K x N and N elements for A, B and bias at a logical
+ * shape; the compiled shapes otherwise), and host_out has room for the result;
+ * the library copies exactly those sizes.  mode is TF_MODE_KERNEL or TF_MODE_BLAS. */
 int tf_run(tf_kernel_t *k, int mode, const long long *logical_mnk, const float *const *host_inputs,
            float *host_out);
 

@@ -60,6 +60,7 @@ SIGNATURES = [
     ("tf_kernel_launch_info", I, [P, I, ctypes.POINTER(LaunchInfo)]),
     ("tf_kernel_num_buffers", I, [P]),
     ("tf_kernel_buffer_info", I, [P, I, ctypes.POINTER(BufferInfo)]),
+    ("tf_kernel_host_shape", I, [P, ctypes.POINTER(LL), I, ctypes.POINTER(LL), ctypes.POINTER(LL)]),
     ("tf_kernel_info", I, [P, I, ctypes.POINTER(KernelResources)]),
     ("tf_launch", I, [P, ctypes.POINTER(P), P]),
     ("tf_run", I, [P, I, ctypes.POINTER(LL), ctypes.POINTER(ctypes.POINTER(ctypes.c_float)),
@@ -147,17 +148,17 @@ class Kernel:
                 "blocks_per_sm": r.blocks_per_cu, "theo_occupancy": round(r.theo_occupancy, 3),
                 "threads": r.threads}
 
-    def _expect_sizes(self, logical):
-        """Element count of each buffer (inputs, then the output) that tf_run
-        reads or writes: the compiled shapes, or for a logical (unpadded) run
-        of a single-matmul program A (M x K), B (K x N), bias (N), C (M x N)."""
-        bufs = self.buffers()
-        if logical is None:
-            return [int(b["shape"][0]) * int(b["shape"][1]) for b in bufs]
-        if len(self.launches()) != 1 or len(bufs) not in (3, 4):
-            return None  # tf_run refuses logical sizes here with its own message
-        m, n, k = (int(x) for x in logical)
-        return [m * k, k * n] + [n] * (len(bufs) - 3) + [m * n]
+    def host_shapes(self, logical=None):
+        """(rows, cols) of each buffer (inputs, then the output) as tf_run and
+        tf_bench copy it: the library's own answer, so the check below and the
+        copies agree (a buffer in two roles, reordered arguments).  Raises the
+        library's error where it would refuse `logical`."""
+        L, out = lib(), []
+        r, c = LL(), LL()
+        for i in range(check(L.tf_kernel_num_buffers(self.h))):
+            check(L.tf_kernel_host_shape(self.h, self._logical(logical), i, ctypes.byref(r), ctypes.byref(c)))
+            out.append((r.value, c.value))
+        return out
 
     def _check_host(self, arrays, out, logical):
         # tf_run copies whole buffers from and to these pointers: a short,
@@ -165,18 +166,24 @@ class Kernel:
         nargs = len(self.buffers()) - 1
         if len(arrays) != nargs:
             raise ValueError(f"this program takes {nargs} input arrays, got {len(arrays)}")
-        want = self._expect_sizes(logical)
-        named = [(f"input {i}", a) for i, a in enumerate(arrays)] + ([("output", out)] if out is not None else [])
-        for i, (what, a) in enumerate(named):
+        want = [r * c for r, c in self.host_shapes(logical)]
+        named = [(f"input {i}", a, want[i]) for i, a in enumerate(arrays)]
+        if out is not None:
+            named.append(("output", out, want[-1]))
+        for what, a, size in named:
             if not isinstance(a, np.ndarray) or a.dtype != np.float32 or not a.flags.c_contiguous:
                 raise TypeError(f"{what} must be a C-contiguous float32 numpy array")
-            if want is not None and a.size != want[i if what != "output" else -1]:
-                raise ValueError(f"{what} has {a.size} elements, the program needs {want[i if what != 'output' else -1]}")
+            if a.size != size:
+                raise ValueError(f"{what} has {a.size} elements, the program needs {size}")
 
     def launch(self, device_ptrs, stream=0):
-        nbuf = len(self.buffers())
-        if len(device_ptrs) != nbuf:
-            raise ValueError(f"this program takes {nbuf} device buffers (inputs, then the output), got {len(device_ptrs)}")
+        bufs = self.buffers()
+        if len(device_ptrs) != len(bufs):
+            raise ValueError(f"this program takes {len(bufs)} device buffers (inputs, then the output), "
+                             f"got {len(device_ptrs)}")
+        for i, (p, b) in enumerate(zip(device_ptrs, bufs)):
+            if not int(p) and b["shape"][0] * b["shape"][1] > 0:
+                raise ValueError(f"device buffer {i} ({b['name']}) is a null pointer")
         arr = (P * len(device_ptrs))(*[P(int(p)) for p in device_ptrs])
         check(lib().tf_launch(self.h, arr, P(int(stream)) if stream else None))
 

@@ -444,6 +444,49 @@ void buffer_2d(const tff::Buffer &b, int64_t &rows, int64_t &cols) {
   for (size_t i = 0; i + 1 < b.shape.size(); ++i) rows *= b.shape[i];
 }
 
+// Host-side 2-D shape of every argN buffer (entry arguments, then the result)
+// as tf_run and tf_bench copy it: the compiled shape, or, with logical sizes
+// (a single-matmul program compiled at a padded shape), the logical shape of
+// the buffer's role in the chain -- A m x k, B k x n, bias 1 x n, residual and
+// C m x n.  An argument with no role keeps its compiled shape.  A buffer with
+// two roles whose logical shapes differ (A reused as the residual with k != n)
+// cannot be padded consistently, and is refused.
+int host_shapes(const tf_kernel *k, const long long *logical, std::vector<int64_t> &rows,
+                std::vector<int64_t> &cols) {
+  const tff::Plan &pl = k->plan;
+  const int nb = pl.nargs + 1;
+  rows.assign(nb, 0);
+  cols.assign(nb, 0);
+  for (int i = 0; i < nb; ++i) buffer_2d(pl.buffers[i], rows[i], cols[i]);
+  if (!logical) return TF_OK;
+  const bool single_gemm = pl.stages.size() == 1 && pl.stages[0].kind == tff::STAGE_GEMM;
+  if (!single_gemm) return fail(TF_E_ARG, "logical (unpadded) sizes apply to single-matmul programs only");
+  const tff::Stage &st = pl.stages[0];
+  const int64_t m = logical[0], n = logical[1], kk = logical[2];
+  if (m <= 0 || n <= 0 || kk <= 0 || m > st.M || n > st.N || kk > st.K)
+    return fail(TF_E_ARG, "padded sizes must be >= M, N, K");
+  std::vector<std::string> role(nb);
+  auto assign = [&](int id, int64_t r, int64_t c, const char *what) {
+    if (id < 0 || id >= nb) return TF_OK;  // an intermediate
+    if (!role[id].empty() && (rows[id] != r || cols[id] != c))
+      return fail(TF_E_ARG, "buffer " + std::to_string(id) + " (" + pl.buffers[id].name + ") is both the " +
+                                role[id] + " and the " + what +
+                                ", whose logical shapes differ; compile the program at its logical shape "
+                                "(mask-edges) instead of padding it");
+    rows[id] = r;
+    cols[id] = c;
+    role[id] = what;
+    return TF_OK;
+  };
+  int rc = assign(st.a, m, kk, "matmul lhs");
+  if (!rc) rc = assign(st.b, kk, n, "matmul rhs");
+  if (!rc) rc = assign(st.out, m, n, "result");
+  for (const tff::EpiOp &e : st.epi)
+    if (!rc && e.buf >= 0)
+      rc = e.kind == tfk::EPI_BIAS ? assign(e.buf, 1, n, "bias") : assign(e.buf, m, n, "add operand");
+  return rc;
+}
+
 int prepare(tf_kernel *k, int mode, const long long *logical, const float *const *host_in, unsigned seed, Exec &ex) {
   ex.k = k;
   ex.mode = mode;
@@ -452,47 +495,19 @@ int prepare(tf_kernel *k, int mode, const long long *logical, const float *const
   if (mode != TF_MODE_KERNEL && mode != TF_MODE_BLAS) return fail(TF_E_ARG, "mode must be TF_MODE_KERNEL or TF_MODE_BLAS");
   const bool single_gemm = pl.stages.size() == 1 && pl.stages[0].kind == tff::STAGE_GEMM;
   if (mode == TF_MODE_BLAS && !single_gemm) return fail(TF_E_BLAS, "blas mode needs a program with one matmul chain");
-  TF_HIP(hipSetDevice(0));
-  TF_HIP(hipStreamCreate(&ex.stream));
-  ex.lrows.resize(nb);
-  ex.lcols.resize(nb);
-  ex.prows.resize(nb);
-  ex.pcols.resize(nb);
-  for (int i = 0; i < nb; ++i) {
-    buffer_2d(pl.buffers[i], ex.prows[i], ex.pcols[i]);
-    ex.lrows[i] = ex.prows[i];
-    ex.lcols[i] = ex.pcols[i];
-  }
+  int rc = host_shapes(k, logical, ex.lrows, ex.lcols);
+  if (rc) return rc;
+  rc = host_shapes(k, nullptr, ex.prows, ex.pcols);
+  if (rc) return rc;
   if (single_gemm) {
     const tff::Stage &st = pl.stages[0];
-    ex.M = st.M;
-    ex.N = st.N;
-    ex.K = st.K;
+    ex.M = logical ? logical[0] : st.M;
+    ex.N = logical ? logical[1] : st.N;
+    ex.K = logical ? logical[2] : st.K;
+    ex.is_padded = mode == TF_MODE_KERNEL && (ex.M != st.M || ex.N != st.N || ex.K != st.K);
   }
-  if (logical) {
-    if (!single_gemm) return fail(TF_E_ARG, "logical (unpadded) sizes apply to single-matmul programs only");
-    const tff::Stage &st = pl.stages[0];
-    const int64_t m = logical[0], n = logical[1], kk = logical[2];
-    if (m <= 0 || n <= 0 || kk <= 0 || m > st.M || n > st.N || kk > st.K)
-      return fail(TF_E_ARG, "padded sizes must be >= M, N, K");
-    ex.M = m;
-    ex.N = n;
-    ex.K = kk;
-    // Logical shape of every buffer from its role in the matmul chain.
-    for (int i = 0; i < nb; ++i) {
-      if (i == st.a) { ex.lrows[i] = m; ex.lcols[i] = kk; }
-      else if (i == st.b) { ex.lrows[i] = kk; ex.lcols[i] = n; }
-      else if (i == st.out) { ex.lrows[i] = m; ex.lcols[i] = n; }
-      else {
-        for (const tff::EpiOp &e : st.epi)
-          if (e.buf == i) {
-            if (e.kind == tfk::EPI_BIAS) { ex.lrows[i] = 1; ex.lcols[i] = n; }
-            else { ex.lrows[i] = m; ex.lcols[i] = n; }
-          }
-      }
-    }
-    ex.is_padded = mode == TF_MODE_KERNEL && (m != st.M || n != st.N || kk != st.K);
-  }
+  TF_HIP(hipSetDevice(0));
+  TF_HIP(hipStreamCreate(&ex.stream));
   ex.logical.resize(nb);
   std::mt19937 rng(seed);
   std::uniform_real_distribution<float> dist(-1.0f, 1.0f);
@@ -712,8 +727,30 @@ int tf_kernel_info(const tf_kernel_t *k, int launch, tf_kernel_resources_t *out)
   return TF_OK;
 }
 
+int tf_kernel_host_shape(const tf_kernel_t *k, const long long *logical_mnk, int index, long long *rows,
+                         long long *cols) {
+  if (!k || !rows || !cols || index < 0 || index > k->plan.nargs) return fail(TF_E_ARG, "bad buffer index");
+  std::vector<int64_t> r, c;
+  int rc = host_shapes(k, logical_mnk, r, c);
+  if (rc) return rc;
+  *rows = r[index];
+  *cols = c[index];
+  return TF_OK;
+}
+
+// A null pointer for a buffer that a launch reads or writes would fault the
+// GPU; it is refused here, before anything is enqueued.
+static int check_buffers(const tf_kernel_t *k, void *const *bufs) {
+  for (int i = 0; i <= k->plan.nargs; ++i)
+    if (!bufs[i] && k->plan.buffers[i].numel() > 0)
+      return fail(TF_E_ARG, "buffer " + std::to_string(i) + " (" + k->plan.buffers[i].name + ") is a null pointer");
+  return TF_OK;
+}
+
 static int launch_impl(tf_kernel_t *k, void *const *device_buffers, void *stream) {
   if (!k || !device_buffers) return fail(TF_E_ARG, "null kernel or buffers");
+  int rc0 = check_buffers(k, device_buffers);
+  if (rc0) return rc0;
   std::vector<void *> ptrs;
   int rc = pointer_table(k, device_buffers, ptrs);
   if (rc) return rc;
@@ -727,6 +764,8 @@ static int launch_impl(tf_kernel_t *k, void *const *device_buffers, void *stream
 static int run_impl(tf_kernel_t *k, int mode, const long long *logical_mnk, const float *const *host_inputs,
                     float *host_out) {
   if (!k || !host_inputs || !host_out) return fail(TF_E_ARG, "null kernel, inputs or output");
+  for (int i = 0; i < k->plan.nargs; ++i)
+    if (!host_inputs[i]) return fail(TF_E_ARG, "host input " + std::to_string(i) + " is a null pointer");
   Exec ex;
   int rc = prepare(k, mode, logical_mnk, host_inputs, 0, ex);
   if (rc) return rc;
@@ -745,6 +784,8 @@ static int run_impl(tf_kernel_t *k, int mode, const long long *logical_mnk, cons
 static int bench_impl(tf_kernel_t *k, int mode, const long long *logical_mnk, const float *const *host_inputs,
                       unsigned seed, int warmup, int reps, int flush, tf_bench_result_t *out) {
   if (!k || !out || warmup < 0 || reps < 1) return fail(TF_E_ARG, "bad bench arguments");
+  for (int i = 0; host_inputs && i < k->plan.nargs; ++i)
+    if (!host_inputs[i]) return fail(TF_E_ARG, "host input " + std::to_string(i) + " is a null pointer");
   Exec ex;
   int rc = prepare(k, mode, logical_mnk, host_inputs, seed, ex);
   if (rc) return rc;

@@ -141,3 +141,74 @@ def test_host_arrays_and_pointer_counts_are_validated():
     with pytest.raises(ValueError, match="input 0 has 1600 elements, the program needs 1500"):
         kp.run([np.zeros((100, 16), np.float32), np.zeros((15, 50), np.float32), np.zeros(50, np.float32)],
                np.zeros((100, 50), np.float32), logical=(100, 50, 15))
+
+
+def _prog(args, body, ret):
+    """A tforge program from (name, dims) arguments, op lines and the result type."""
+    t = lambda *d: "tensor<" + "x".join(str(x) for x in d) + "xf32>"
+    head = ", ".join(f"%{n}: {t(*d)}" for n, d in args)
+    return f"func.func @entry({head}) -> {t(*ret)} {{\n" + "".join(f"  {l}\n" for l in body) + \
+        f"  return %{len(body) - 1} : {t(*ret)}\n}}\n"
+
+
+STAGED_16 = "block-tile=64,64 thread-tile=4,4 tile-k=16 promote=1 vectorize=1"
+
+
+def test_host_shapes_follow_roles_not_positions():
+    """The library reports each buffer's host shape from its role in the chain,
+    and the Python mirror checks arrays against that report: an add residual is
+    m x n (not a bias), and reordered arguments keep their own roles."""
+    from tensorforge_amd import _lib
+    t = "tensor<64x32xf32>, tensor<32x64xf32> -> tensor<64x64xf32>"
+    resid = _prog([("a", (64, 32)), ("b", (32, 64)), ("r", (64, 64))],
+                  [f"%0 = tforge.matmul %a, %b : {t}",
+                   "%1 = tforge.add %0, %r : tensor<64x64xf32>, tensor<64x64xf32> -> tensor<64x64xf32>"], (64, 64))
+    k = _lib.Kernel(resid, STAGED_16)
+    assert k.host_shapes() == [(64, 32), (32, 64), (64, 64), (64, 64)]
+    assert k.host_shapes((50, 50, 20)) == [(50, 20), (20, 50), (50, 50), (50, 50)]
+    with pytest.raises(ValueError, match="input 2 has 50 elements, the program needs 2500"):
+        k.run([np.zeros((50, 20), np.float32), np.zeros((20, 50), np.float32), np.zeros(50, np.float32)],
+              np.zeros((50, 50), np.float32), logical=(50, 50, 20))
+    swapped = _prog([("b", (32, 64)), ("a", (64, 32))], [f"%0 = tforge.matmul %a, %b : {t}"], (64, 64))
+    k = _lib.Kernel(swapped, STAGED_16)
+    assert k.host_shapes((50, 40, 20)) == [(20, 40), (50, 20), (50, 40)]
+    with pytest.raises(ValueError, match="input 0 has 1000 elements, the program needs 800"):
+        k.run([np.zeros((50, 20), np.float32), np.zeros((20, 40), np.float32)], np.zeros((50, 40), np.float32),
+              logical=(50, 40, 20))
+
+
+def test_buffer_in_two_roles_refuses_inconsistent_logical_sizes():
+    """A reused as the residual (K == N when compiled): logical sizes with
+    k != n would need two different pads of one buffer, so the library refuses
+    them; with k == n the two roles agree and the sizes are accepted."""
+    from tensorforge_amd import _lib
+    t = "tensor<64x64xf32>"
+    prog = _prog([("a", (64, 64)), ("b", (64, 64))],
+                 [f"%0 = tforge.matmul %a, %b : {t}, {t} -> {t}", f"%1 = tforge.add %0, %a : {t}, {t} -> {t}"],
+                 (64, 64))
+    k = _lib.Kernel(prog, STAGED_16)
+    with pytest.raises(RuntimeError, match=r"buffer 0 \(%a\) is both the matmul lhs and the add operand"):
+        k.host_shapes((50, 50, 20))
+    assert k.host_shapes((50, 40, 40)) == [(50, 40), (40, 40), (50, 40)]
+    with pytest.raises(RuntimeError, match="single-matmul programs only"):
+        _lib.Kernel(tc.gen_mlir("resmlp", 64, 64, 64), STAGED_16).host_shapes((60, 60, 60))
+    with pytest.raises(RuntimeError, match="padded sizes must be >= M, N, K"):
+        k.host_shapes((65, 64, 64))
+
+
+def test_null_device_pointer_is_refused_before_any_launch():
+    """A null buffer would fault the GPU; the library refuses it before it
+    touches the device (so this runs without one), and so does the mirror."""
+    import ctypes
+    from tensorforge_amd import _lib
+    k = _lib.Kernel(tc.gen_mlir("mbr", 64, 64, 64), STAGED_16)
+    with pytest.raises(ValueError, match=r"device buffer 2 \(%bias\) is a null pointer"):
+        k.launch([16, 32, 0, 48])
+    L = _lib.lib()
+    arr = (ctypes.c_void_p * 4)(16, 32, None, 48)
+    assert L.tf_launch(k.h, arr, None) == -4
+    assert b"buffer 2 (%bias) is a null pointer" in L.tf_last_error()
+    ins = (ctypes.POINTER(ctypes.c_float) * 3)()
+    out = np.zeros((64, 64), np.float32)
+    assert L.tf_run(k.h, 0, None, ins, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))) == -4
+    assert b"host input 0 is a null pointer" in L.tf_last_error()
