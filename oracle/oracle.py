@@ -19,12 +19,25 @@ Contents, each a restatement of the reference (paths in the TensorForge tree):
   matmul_fma / matmul_nofma / epilogue   C closed forms in tforge_oracle.c;
       pinned bit-for-bit by the e1 bitwise-difference counts.
   e1_metrics(out, ref, bound)            bench/e1_numerics.py:93-104
+  preactivation64(ins)                   z = A64 @ B64 + bias64, the value whose
+      sign the ReLU decides (lib/Conversion/TForgeToLinalg.cpp:94-133); pinned
+      bit for bit to fp64_reference (max(z, 0) is its ref) and to exact integer
+      arithmetic on a small case.
+  mask_mismatches(out, z, bound)         the north star's ReLU-mask gate: where
+      |z| > bound, out == 0 must agree with z <= 0; pinned by planted flips
+      (each counts exactly once), in-bound perturbations (count nothing) and
+      |z| == bound exactly (undecided).
+  add / relu / bias_add                  tforge.add / relu / bias_add on their
+      own (docs/dialect.md:26-30; python/tforge_gpu.py:116-126): one IEEE f32
+      op per element, relu = maximum(x, +0.0) with NaN kept and -0 -> +0;
+      pinned against NumPy float32 on NaN, +-0, +-inf, denormals and overflow.
   mbr_vec6x16 / matmul_scalar_mnk / time_*   the CPU baseline port and the default
       scalar pipeline's loop (tforge_oracle.c); pinned by the err/bound the reference's
       CPU results hold for both (results/cpu/stage4.csv, stage6_best.csv).
 
 Nothing here is "parity unpinned": every function above has a known-answer
-test against files the reference itself holds (tests/test_oracle_golden.py).
+test against files the reference itself holds or against what the
+mathematics fixes (tests/test_oracle_golden.py, tests/test_oracle_pins.py).
 """
 
 import ctypes
@@ -73,6 +86,8 @@ def lib():
     L.tfo_add.argtypes = [fp, fp, fp, i64]
     L.tfo_relu.argtypes = [fp, fp, i64]
     L.tfo_bias_add.argtypes = [fp, fp, fp, i64, i64]
+    for fn in ("tfo_add", "tfo_relu", "tfo_bias_add"):
+        getattr(L, fn).restype = None
     L.tfo_mbr_vec6x16.argtypes = [fp, fp, fp, fp, i64, i64, i64, i32, i32]
     L.tfo_mbr_vec6x16.restype = None
     for fn in ("tfo_time_mbr_vec6x16", "tfo_time_scalar"):
@@ -144,6 +159,44 @@ def epilogue(c, bias=None, relu=False, resid=None):
     resid = None if resid is None else _f32(resid)
     lib().tfo_epilogue(_p(y), _p(bias), _p(resid), m, n, flags)
     return y
+
+
+def add(x, y):
+    """tforge.add: x + y, one f32 rounding per element (tfo_add)."""
+    x, y = _f32(x), _f32(y)
+    assert x.shape == y.shape
+    out = np.empty_like(x)
+    lib().tfo_add(_p(x), _p(y), _p(out), x.size)
+    return out
+
+
+def relu(x):
+    """tforge.relu: maximum(x, +0.0) -- NaN stays NaN, -0.0 becomes +0.0 (tfo_relu)."""
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().tfo_relu(_p(x), _p(out), x.size)
+    return out
+
+
+def bias_add(x, bias):
+    """tforge.bias_add: x[m, n] + bias[n] along the last dimension (tfo_bias_add)."""
+    x, bias = _f32(x), _f32(bias)
+    m, n = x.shape
+    assert bias.shape == (n,)
+    out = np.empty_like(x)
+    lib().tfo_bias_add(_p(x), _p(bias), _p(out), m, n)
+    return out
+
+
+def elementwise(workload, ins):
+    """Expected output of an element-op workload on make_inputs-style arrays."""
+    if workload == "add":
+        return add(ins["a"], ins["b"])
+    if workload == "relu":
+        return relu(ins["a"])
+    if workload == "bias_add":
+        return bias_add(ins["a"], ins["bias"])
+    raise ValueError(workload)
 
 
 def mbr_fma(a, b, bias, threads=0):

@@ -171,8 +171,9 @@ def test_random_element_op(workload, shape, opts):
     m, n = shape
     print(f"draw {workload} {shape} {opts}", flush=True)
     d, launch = tg.compile_kernel(workload, m, n, None, opts, tag="test")
-    res, _ = tg.check(workload, m, n, None, d, launch)
+    res, out = tg.check(workload, m, n, None, d, launch)
     assert res["pass"], res
+    assert o.bitwise_diff(out, o.elementwise(workload, o.make_inputs(workload, m, n, None))) == 0
 
 
 @pytest.mark.parametrize("shape,cfg", RESMLP_DRAWS,
