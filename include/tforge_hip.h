@@ -174,11 +174,21 @@ int tf_run(tf_kernel_t *k, int mode, const long long *logical_mnk, const float *
 /* Timing run: inputs from `host_inputs` (or, if NULL, uniform[-1,1] from
  * `seed`), `warmup` untimed runs, then `reps` runs each bracketed by a HIP
  * event pair on the library's stream (pad copies included when padded, an
- * optional 512 MiB L2/MALL flush before each rep outside the events), GPU
- * clock and power sampled after each rep.  Replaces
+ * optional 512 MiB L2/MALL flush before each rep outside the events), the
+ * shader clock (tf_clock_probe) and, where amdsmi loads, the power sampled
+ * after each rep.  Replaces
  * runners/gpu/tforge-gpu-bench.cu:337-381. */
 int tf_bench(tf_kernel_t *k, int mode, const long long *logical_mnk, const float *const *host_inputs,
              unsigned seed, int warmup, int reps, int flush, tf_bench_result_t *out);
+
+/* Shader clock (MHz) measured on the device: a probe kernel after the work
+ * already queued on `stream` (a hipStream_t, NULL for the default stream)
+ * counts shader-clock cycles against the 100 MHz wall clock in one workgroup
+ * per XCD; mean, min and max over the XCDs (min/max may be NULL).
+ * Synchronises the stream.  tf_bench takes one such sample after every rep;
+ * the reference samples the SM clock through NVML instead
+ * (runners/gpu/tforge-gpu-bench.cu:333-361). */
+int tf_clock_probe(void *stream, double *mean_mhz, double *min_mhz, double *max_mhz);
 
 /* Per-rep event times (ms) of the last tf_bench on this handle, up to `cap`
  * values; returns the count.  No counterpart in the reference (its runner

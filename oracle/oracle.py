@@ -213,19 +213,40 @@ def mbr_vec6x16(a, b, bias=None, relu=True, threads=0):
     return c
 
 
-def time_vec6x16(a, b, bias, warmup, reps):
-    """Median ns per call, one pinned-free thread, of the 6x16x4 port."""
-    a, b, bias = _f32(a), _f32(b), _f32(bias)
-    (m, k), (_, n) = a.shape, b.shape
-    c = np.empty((m, n), np.float32)
-    return lib().tfo_time_mbr_vec6x16(_p(a), _p(b), _p(bias), _p(c), m, n, k, BIAS | RELU, warmup, reps)
+def aligned_empty(shape, align=64):
+    """An uninitialised float32 array whose data starts on an `align`-byte
+    boundary (the reference CPU runner's buffers are 64-byte aligned:
+    runners/cpu/tforge-cpu-bench.cpp:65-77)."""
+    size = int(np.prod(shape))
+    raw = np.empty(size + align // 4, np.float32)
+    off = (-raw.ctypes.data % align) // 4
+    return raw[off:off + size].reshape(shape)
 
 
-def time_scalar(a, b, bias, warmup, reps):
-    a, b, bias = _f32(a), _f32(b), _f32(bias)
+def aligned_copy(x, align=64):
+    out = aligned_empty(np.shape(x), align)
+    out[...] = x
+    return out
+
+
+def _timing_args(a, b, bias, relu):
+    a, b = _f32(a), _f32(b)
     (m, k), (_, n) = a.shape, b.shape
-    c = np.empty((m, n), np.float32)
-    return lib().tfo_time_scalar(_p(a), _p(b), _p(bias), _p(c), m, n, k, BIAS | RELU, warmup, reps)
+    flags = (BIAS if bias is not None else 0) | (RELU if relu else 0)
+    return a, b, (None if bias is None else _f32(bias)), aligned_empty((m, n)), m, n, k, flags
+
+
+def time_vec6x16(a, b, bias, warmup, reps, relu=True):
+    """Median ns per call of the 6x16x4 port, one thread, on the calling
+    thread's CPU (the caller pins it); bias None and relu False time plain matmul."""
+    a, b, bias, c, m, n, k, flags = _timing_args(a, b, bias, relu)
+    return lib().tfo_time_mbr_vec6x16(_p(a), _p(b), _p(bias), _p(c), m, n, k, flags, warmup, reps)
+
+
+def time_scalar(a, b, bias, warmup, reps, relu=True):
+    """Median ns per call of the default pipeline's scalar loop + epilogue."""
+    a, b, bias, c, m, n, k, flags = _timing_args(a, b, bias, relu)
+    return lib().tfo_time_scalar(_p(a), _p(b), _p(bias), _p(c), m, n, k, flags, warmup, reps)
 
 
 def fp64_reference(workload, ins):

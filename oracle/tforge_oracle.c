@@ -267,7 +267,7 @@ double tfo_time_scalar(const float *A, const float *B, const float *bias, float 
     struct timespec t0, t1;
     clock_gettime(CLOCK_MONOTONIC, &t0);
     tfo_matmul_scalar_mnk(A, B, C, M, N, K);
-    tfo_epilogue(C, bias, 0, M, N, flags);
+    if (flags) tfo_epilogue(C, bias, 0, M, N, flags);
     clock_gettime(CLOCK_MONOTONIC, &t1);
     if (i >= warmup) ts[i - warmup] = (t1.tv_sec - t0.tv_sec) * 1e9 + (t1.tv_nsec - t0.tv_nsec);
   }

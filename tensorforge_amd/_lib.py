@@ -67,6 +67,8 @@ SIGNATURES = [
                    ctypes.POINTER(ctypes.c_float)]),
     ("tf_bench", I, [P, I, ctypes.POINTER(LL), ctypes.POINTER(ctypes.POINTER(ctypes.c_float)), U, I, I, I,
                      ctypes.POINTER(BenchResult)]),
+    ("tf_clock_probe", I, [P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+                           ctypes.POINTER(ctypes.c_double)]),
     ("tf_bench_samples", I, [P, ctypes.POINTER(ctypes.c_double), I]),
     ("tf_registry_size", I, []),
     ("tf_registry_entry", I, [I, ctypes.POINTER(I), ctypes.POINTER(I), ctypes.c_char_p, I]),
@@ -227,6 +229,14 @@ def device_info():
             "max_threads_per_cu": d.max_threads_per_cu, "l2_bytes": d.l2_bytes,
             "global_mem_bytes": d.global_mem_bytes, "driver_version": d.driver_version,
             "runtime_version": d.runtime_version}
+
+
+def clock_probe(stream=0):
+    """Shader clock in MHz (mean, min, max over the XCDs), measured on the
+    device after the work queued on `stream`; synchronises that stream."""
+    v = [ctypes.c_double() for _ in range(3)]
+    check(lib().tf_clock_probe(P(int(stream)) if stream else None, *(ctypes.byref(x) for x in v)))
+    return tuple(x.value for x in v)
 
 
 def registry():

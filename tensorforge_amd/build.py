@@ -5,7 +5,8 @@ compile every translation unit in parallel (hipcc for HIP, g++ for the host
 front end), link the shared library next to this file, and record each
 kernel's register / LDS / scratch usage from the compiler's resource remarks
 in kernel_resources.json (the counterpart of the reference's ptxas -v report,
-python/tforge_gpu.py:155-160).
+python/tforge_gpu.py:155-160), and the commit the library was built from in
+BUILD_INFO.json (results rows name it; the GPU machine gets no .git).
 
     python -m tensorforge_amd.build [--no-force] [-j N]
 """
@@ -128,6 +129,9 @@ def build(force=True, jobs=None):
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
     os.replace(tmp, LIB)
     RESOURCES.write_text(json.dumps(_resources([t for _, t in results]), indent=1, sort_keys=True) + "\n")
+    sys.path.insert(0, str(ROOT))
+    from tensorforge_amd import provenance
+    provenance.write_build_info()
     return LIB
 
 

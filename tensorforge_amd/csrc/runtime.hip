@@ -296,8 +296,10 @@ int pointer_table(tf_kernel *k, void *const *bufs, std::vector<void *> &ptrs) {
 
 // ------------------------------------------------------------ runner ---
 
-// amdsmi, loaded lazily: GPU clock and power per rep, as the reference samples
-// NVML (runners/gpu/tforge-gpu-bench.cu:333-361).  Missing -> -1.
+// amdsmi, loaded lazily: socket power per rep, as the reference samples NVML
+// (runners/gpu/tforge-gpu-bench.cu:333-361).  Missing -> -1.  (The clock comes
+// from clock_probe: amdsmi's current clock, read once a short rep has ended,
+// is already the idle clock.)
 struct Smi {
   bool ok = false;
   void *h = nullptr;
@@ -305,11 +307,6 @@ struct Smi {
   typedef int (*init_t)(uint64_t);
   typedef int (*sockets_t)(uint32_t *, void **);
   typedef int (*procs_t)(void *, uint32_t *, void **);
-  struct clk_t {
-    uint32_t clk, min_clk, max_clk;
-    uint8_t locked, deep_sleep;
-    uint32_t reserved[4];
-  };
   struct pwr_t {
     uint64_t socket_power;
     uint32_t current_socket_power, average_socket_power;
@@ -317,9 +314,7 @@ struct Smi {
     uint32_t power_limit;
     uint64_t reserved[18];
   };
-  typedef int (*clock_t_)(void *, int, clk_t *);
   typedef int (*power_t)(void *, pwr_t *);
-  clock_t_ get_clock = nullptr;
   power_t get_power = nullptr;
 
   Smi() {
@@ -330,9 +325,8 @@ struct Smi {
     auto init = (init_t)dlsym(h, "amdsmi_init");
     auto sockets = (sockets_t)dlsym(h, "amdsmi_get_socket_handles");
     auto procs = (procs_t)dlsym(h, "amdsmi_get_processor_handles");
-    get_clock = (clock_t_)dlsym(h, "amdsmi_get_clock_info");
     get_power = (power_t)dlsym(h, "amdsmi_get_power_info");
-    if (!init || !sockets || !procs || !get_clock || init(1u << 1) != 0) return;
+    if (!init || !sockets || !procs || !get_power || init(1u << 1) != 0) return;
     uint32_t ns = 0;
     if (sockets(&ns, nullptr) != 0 || ns == 0) return;
     std::vector<void *> socks(ns);
@@ -346,11 +340,6 @@ struct Smi {
       break;
     }
     ok = proc != nullptr;
-  }
-  double clock_mhz() {
-    clk_t c{};
-    if (!ok || get_clock(proc, 0 /* GFX */, &c) != 0) return -1;
-    return c.clk;
   }
   double power_w() {
     pwr_t p{};
@@ -414,6 +403,54 @@ Stats stats(std::vector<double> v) {
   for (double x : v) var += (x - mean) * (x - mean);
   const double med = n % 2 ? v[n / 2] : 0.5 * (v[n / 2 - 1] + v[n / 2]);
   return {med, v.front(), mean, n > 1 ? std::sqrt(var / (n - 1)) : 0.0};
+}
+
+// Shader-clock probe: each workgroup (one per XCD: workgroups are dealt to the
+// 8 XCDs round-robin) spins for 4 us of the 100 MHz wall clock and records the
+// shader-clock cycles (s_memtime) that passed meanwhile.  The spin also ends
+// after 2^20 reads, so the kernel exits whatever the counters do.
+constexpr int kProbeGroups = 8;
+__device__ unsigned long long g_clock_probe[2 * kProbeGroups];
+
+__global__ void clock_probe_kernel(unsigned long long *out) {
+  if (threadIdx.x != 0) return;
+  const unsigned long long w0 = wall_clock64(), c0 = clock64();
+  unsigned long long w1 = w0;
+  for (int i = 0; i < (1 << 20) && w1 - w0 < 400; ++i) w1 = wall_clock64();
+  const unsigned long long c1 = clock64();
+  out[2 * blockIdx.x] = c1 - c0;
+  out[2 * blockIdx.x + 1] = w1 - w0;
+}
+
+// Mean, min and max shader clock (MHz) over the XCDs, measured on `stream`
+// after the work already queued there.  Synchronises the stream.
+int clock_probe(hipStream_t stream, double &mean, double &mn, double &mx) {
+  static thread_local int probe_dev = -1;
+  static thread_local unsigned long long *probe_ptr = nullptr;
+  static thread_local int wall_khz = 0;
+  int dev = 0;
+  TF_HIP(hipGetDevice(&dev));
+  if (dev != probe_dev) {
+    TF_HIP(hipGetSymbolAddress(reinterpret_cast<void **>(&probe_ptr), HIP_SYMBOL(g_clock_probe)));
+    TF_HIP(hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, dev));
+    probe_dev = dev;
+  }
+  hipLaunchKernelGGL(clock_probe_kernel, dim3(kProbeGroups), dim3(64), 0, stream, probe_ptr);
+  TF_HIP(hipGetLastError());
+  unsigned long long h[2 * kProbeGroups];
+  TF_HIP(hipMemcpyAsync(h, probe_ptr, sizeof(h), hipMemcpyDeviceToHost, stream));
+  TF_HIP(hipStreamSynchronize(stream));
+  mean = 0;
+  mn = 1e30;
+  mx = 0;
+  for (int g = 0; g < kProbeGroups; ++g) {
+    if (h[2 * g + 1] == 0) return fail(TF_E_HIP, "clock probe: the wall clock did not advance");
+    const double mhz = double(h[2 * g]) * wall_khz / (double(h[2 * g + 1]) * 1000.0);
+    mean += mhz / kProbeGroups;
+    mn = std::min(mn, mhz);
+    mx = std::max(mx, mhz);
+  }
+  return TF_OK;
 }
 
 __global__ void fill_u32(uint32_t *p, size_t n, uint32_t v) {
@@ -823,10 +860,13 @@ static int bench_impl(tf_kernel_t *k, int mode, const long long *logical_mnk, co
     float t = 0;
     TF_HIP(hipEventElapsedTime(&t, e0, e1));
     ms[i] = t;
-    // Sampled after the rep's event completes; a reading under 500 MHz is the
-    // GPU already dropping to its idle state, not the clock the rep ran at.
-    const double c = s.clock_mhz(), p = s.power_w();
-    if (c >= 500) clk.push_back(c);
+    // The shader clock right after the rep, measured on the device (the
+    // reference samples NVML per rep); power from amdsmi where it loads.
+    double c = 0, cmin = 0, cmax = 0;
+    rc = clock_probe(ex.stream, c, cmin, cmax);
+    if (rc) return rc;
+    clk.push_back(c);
+    const double p = s.power_w();
     if (p > 0) pwr.push_back(p);
   }
   TF_HIP(hipGetLastError());
@@ -853,6 +893,17 @@ static int bench_impl(tf_kernel_t *k, int mode, const long long *logical_mnk, co
     out->padded[2] = ex.K;
   }
   k->samples = ms;
+  return TF_OK;
+}
+
+int tf_clock_probe(void *stream, double *mean_mhz, double *min_mhz, double *max_mhz) {
+  if (!mean_mhz) return fail(TF_E_ARG, "null output");
+  double mean = 0, mn = 0, mx = 0;
+  int rc = clock_probe(static_cast<hipStream_t>(stream), mean, mn, mx);
+  if (rc) return rc;
+  *mean_mhz = mean;
+  if (min_mhz) *min_mhz = mn;
+  if (max_mhz) *max_mhz = mx;
   return TF_OK;
 }
 

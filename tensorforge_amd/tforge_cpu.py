@@ -1,6 +1,6 @@
 """Workload programs, seeded inputs and shared constants of the TensorForge
 drivers (the parts of the reference's python/tforge_cpu.py that the GPU path
-uses: python/tforge_cpu.py:26, 29-53, 56-62, 89-100, 314-319).
+uses: python/tforge_cpu.py:26, 29-53, 89-100, 154-159).
 
 Workloads and their entry signatures (tensors, row-major f32):
   add      entry(a: MxN, b: MxN) -> MxN
@@ -18,8 +18,6 @@ test oracle.
 """
 
 import pathlib
-import shlex
-import subprocess
 
 import numpy as np
 
@@ -74,15 +72,6 @@ def gen_mlir(workload, m, n, k=None):
     raise ValueError(workload)
 
 
-def run(cmd, **kw):
-    cmd = [str(c) for c in cmd]
-    kw.setdefault("timeout", 600)  # a hung step fails, as in the reference
-    r = subprocess.run(cmd, capture_output=True, text=True, **kw)
-    if r.returncode != 0:
-        raise RuntimeError(f"command failed ({r.returncode}): {shlex.join(cmd)}\n{r.stderr}")
-    return r.stdout
-
-
 def make_inputs(workload, m, n, k, seed=1234):
     """Seeded inputs in entry-argument order (python/tforge_cpu.py:89-100).
 
@@ -112,11 +101,22 @@ def make_inputs(workload, m, n, k, seed=1234):
     raise ValueError(workload)
 
 
+# Work per call that the rate metrics divide by: FP32 FLOPs of the matrix
+# products (2 per multiply-add; the epilogue's adds and maxima are not counted,
+# as in the reference's tables), or the compulsory bytes an element op moves
+# (every input read once, the output written once).
+_WORK = {
+    "matmul": ("GFLOP/s", lambda m, n, k: 2.0 * m * n * k),
+    "mbr": ("GFLOP/s", lambda m, n, k: 2.0 * m * n * k),
+    "resmlp": ("GFLOP/s", lambda m, n, k: 2 * (2.0 * m * n * k)),  # two products of m*n*k each
+    "add": ("GB/s", lambda m, n, k: 4.0 * 3 * m * n),
+    "relu": ("GB/s", lambda m, n, k: 4.0 * 2 * m * n),
+    "bias_add": ("GB/s", lambda m, n, k: 4.0 * 2 * m * n),
+}
+
+
 def flops_or_bytes(workload, m, n, k):
-    """(metric name, amount of work) for the derived metric."""
-    if workload in ("matmul", "mbr"):
-        return "GFLOP/s", 2.0 * m * n * k
-    if workload == "resmlp":
-        return "GFLOP/s", 4.0 * m * n * k
-    arrays = 3 if workload == "add" else 2
-    return "GB/s", arrays * m * n * 4.0
+    """(rate unit, work per call) of a workload (python/tforge_cpu.py:154-159
+    defines the same pair for the reference's four workloads)."""
+    unit, work = _WORK[workload]
+    return unit, work(m, n, k or 0)

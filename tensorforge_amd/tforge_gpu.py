@@ -45,10 +45,6 @@ def fp32_peak_gflops(clock_mhz):
 FP32_PEAK_TFLOPS = fp32_peak_gflops(PEAK_CLOCK_MHZ) / 1e3  # 157.3 TFLOP/s, the published figure
 
 
-def run(cmd, **kw):
-    return tc.run(cmd, **kw)
-
-
 def parse_launch(path):
     """launch.json of a compiled kernel (python/tforge_gpu.py:42-51 parsed the
     tforge.launch attribute of device.mlir; the backend writes it as JSON)."""

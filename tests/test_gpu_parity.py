@@ -429,3 +429,25 @@ def test_info_and_bench_keys():
     for key in ("gpu", "median_ms", "min_ms", "std_ms", "sm_clock_median_mhz", "padded", "grid", "block"):
         assert key in r
     assert r["median_ms"] > 0
+
+
+def test_bench_with_l2_flush_is_not_faster():
+    """--flush (ref:runners/gpu/tforge-gpu-bench.cu:337-350): a 512 MiB fill
+    before every rep evicts A and B from L2 and the MALL, so the flushed
+    median cannot beat the warm one (small tolerance for clock noise)."""
+    m = n = k = 1024
+    d, launch = tg.compile_kernel("mbr", m, n, k, STAGED.format(64, 64, 4, 2, 64), tag="test")
+    warm = tg.bench("mbr", m, n, k, d, launch, warmup=20, reps=50)
+    cold = tg.bench("mbr", m, n, k, d, launch, warmup=20, reps=50, flush=True)
+    assert cold["l2_flush"] == 1 and warm["l2_flush"] == 0
+    assert cold["median_ms"] >= 0.97 * warm["median_ms"], (cold["median_ms"], warm["median_ms"])
+
+
+def test_clock_probe_reads_the_shader_clock():
+    """The device probe reads a plausible MI355X shader clock on every XCD,
+    and tf_bench reports one sample per rep from it."""
+    mean, lo, hi = _lib.clock_probe()
+    assert 100.0 <= lo <= mean <= hi <= 3000.0, (mean, lo, hi)
+    d, launch = tg.compile_kernel("mbr", 512, 512, 512, STAGED.format(64, 64, 4, 2, 64), tag="test")
+    r = tg.bench("mbr", 512, 512, 512, d, launch, warmup=5, reps=20)
+    assert 100.0 <= r["sm_clock_min_mhz"] <= r["sm_clock_median_mhz"] <= r["sm_clock_max_mhz"] <= 3000.0, r

@@ -103,10 +103,33 @@ def test_provenance_fields_are_the_reference_schema(tmp_path):
         "workload", "shape", "dtype", "pipeline", "params", "threads", "warmup", "reps",
         "median_ms", "min_ms", "std_ms", "metric", "metric_value", "sm_clock_median_mhz",
         "clock_adjusted_metric", "alloc_bytes_per_call", "correctness", "notes"]
-    w = provenance.CsvWriter(tmp_path / "x.csv")
-    w.row(commit="c", workload="mbr")
+    t = provenance.ResultsTable(tmp_path / "x.csv", device="dev")
+    t.add(workload="mbr", shape="1x2x3")
+    t.add(workload="relu", device="other")
     with pytest.raises(KeyError):
-        w.row(bogus=1)
+        t.add(bogus=1)
+    with pytest.raises(KeyError):
+        provenance.ResultsTable(tmp_path / "y.csv", bogus=1)
+    t.close()
+    import csv
+    rows = list(csv.DictReader(open(tmp_path / "x.csv")))
+    assert [r["workload"] for r in rows] == ["mbr", "relu"] and [r["device"] for r in rows] == ["dev", "other"]
+    assert rows[0]["commit"] == provenance.commit_label() and rows[0]["shape"] == "1x2x3"
+    provenance.ResultsTable(tmp_path / "x.csv").add(workload="add")  # appends, no second header
+    assert len(list(csv.DictReader(open(tmp_path / "x.csv")))) == 3
+
+
+def test_build_info_names_the_commit(tmp_path, monkeypatch):
+    """The build records HEAD (and whether the tree differed from it) next to
+    the library; rows read it there, so a copy without .git still names it."""
+    info = provenance.write_build_info(tmp_path / "BUILD_INFO.json")
+    assert len(info["commit"]) == 40 and info["commit"] == provenance.git_head()
+    monkeypatch.setattr(provenance, "BUILD_INFO", tmp_path / "BUILD_INFO.json")
+    monkeypatch.setattr(provenance, "ROOT", tmp_path)  # no .git here: only the file can answer
+    assert provenance.commit_label().startswith(info["commit"][:12])
+    assert provenance.commit_label().endswith("-dirty") == bool(info["dirty"])
+    assert provenance.device_label({"name": "AMD Instinct MI355X", "arch": "gfx950:sramecc+:xnack-",
+                                    "compute_units": 256}) == "AMD Instinct MI355X [gfx950:sramecc+:xnack-, 256 CUs]"
 
 
 def test_flops_convention():
