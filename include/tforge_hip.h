@@ -157,6 +157,19 @@ int tf_kernel_info(const tf_kernel_t *k, int launch, tf_kernel_resources_t *out)
  * (runners/gpu/tforge-gpu-bench.cu:259-299). */
 int tf_launch(tf_kernel_t *k, void *const *device_buffers, void *stream);
 
+/* tf_launch without any device allocation, for callers that cannot allocate
+ * (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments and kernels as
+ * tf_launch; the split-K workspace and the intermediates of multi-launch
+ * programs come from one fixed 32 MiB device array per GPU (held from the
+ * library's first use on that GPU until the process ends) instead of the
+ * handle's buffers.  A program that needs more scratch than that is refused
+ * with TF_E_ARG before anything is enqueued.  Nothing in the array needs
+ * clearing between calls (every slice and intermediate is written whole
+ * before it is read), but every call on one GPU shares it: calls that overlap
+ * on that GPU -- from any handle or stream -- race, so serialise them. */
+int tf_launch_noalloc(tf_kernel_t *k, void *const *device_buffers, void *stream);
+
 /* Correctness run, as the runner's "--warmup 0 --reps 1 --in-dir --out":
  * uploads host inputs, NaN-prefills the output, runs once, downloads the
  * result.  `logical_mnk` (may be NULL) gives the unpadded M, N, K of a

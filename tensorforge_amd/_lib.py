@@ -63,6 +63,7 @@ SIGNATURES = [
     ("tf_kernel_host_shape", I, [P, ctypes.POINTER(LL), I, ctypes.POINTER(LL), ctypes.POINTER(LL)]),
     ("tf_kernel_info", I, [P, I, ctypes.POINTER(KernelResources)]),
     ("tf_launch", I, [P, ctypes.POINTER(P), P]),
+    ("tf_launch_noalloc", I, [P, ctypes.POINTER(P), P]),
     ("tf_run", I, [P, I, ctypes.POINTER(LL), ctypes.POINTER(ctypes.POINTER(ctypes.c_float)),
                    ctypes.POINTER(ctypes.c_float)]),
     ("tf_bench", I, [P, I, ctypes.POINTER(LL), ctypes.POINTER(ctypes.POINTER(ctypes.c_float)), U, I, I, I,
@@ -188,6 +189,14 @@ class Kernel:
                 raise ValueError(f"device buffer {i} ({b['name']}) is a null pointer")
         arr = (P * len(device_ptrs))(*[P(int(p)) for p in device_ptrs])
         check(lib().tf_launch(self.h, arr, P(int(stream)) if stream else None))
+
+    def launch_noalloc(self, device_ptrs, stream=0):
+        """tf_launch_noalloc: the same launches with the library's fixed
+        per-GPU scratch array; calls that overlap on one GPU race."""
+        if len(device_ptrs) != len(self.buffers()):
+            raise ValueError(f"this program takes {len(self.buffers())} device buffers, got {len(device_ptrs)}")
+        arr = (P * len(device_ptrs))(*[P(int(p)) for p in device_ptrs])
+        check(lib().tf_launch_noalloc(self.h, arr, P(int(stream)) if stream else None))
 
     @staticmethod
     def _host_ptrs(arrays):

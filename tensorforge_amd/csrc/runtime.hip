@@ -11,6 +11,7 @@
 #include <cstring>
 #include <functional>
 #include <memory>
+#include <mutex>
 #include <new>
 #include <random>
 #include <stdexcept>
@@ -201,7 +202,9 @@ tfk::EpiParams make_epi(const tff::Stage &st, void *const *ptrs) {
   return e;
 }
 
-int launch_stage(const tf_kernel *k, size_t s, void *const *ptrs, hipStream_t stream) {
+// Enqueues stage s of k.  `ptrs` holds every buffer id's device pointer and
+// `ws` the split-K workspace (k->ws_bytes bytes, or null when unused).
+int launch_stage(const tf_kernel *k, size_t s, void *const *ptrs, void *ws, hipStream_t stream) {
   const tff::Stage &st = k->plan.stages[s];
   const Launch &L = k->launches[s];
   if (st.M == 0 || st.N == 0) return TF_OK;
@@ -231,7 +234,7 @@ int launch_stage(const tf_kernel *k, size_t s, void *const *ptrs, hipStream_t st
     p.swizzle = k->opts.xcd_swizzle ? 1 : 0;
     p.splits = (int)L.grid.z;
     if (p.splits > 1) {
-      p.ws = static_cast<float *>(k->ws);
+      p.ws = static_cast<float *>(ws);
       p.ws_ld = (long)L.grid.x * L.entry->bn;
       p.ws_slice = p.ws_ld * L.grid.y * L.entry->bm;
     }
@@ -623,7 +626,7 @@ int run_once(Exec &ex) {
                               ex.lrows[i], hipMemcpyDeviceToDevice, ex.stream));
   }
   for (size_t s = 0; s < pl.stages.size(); ++s) {
-    int rc = launch_stage(k, s, ex.ptrs.data(), ex.stream);
+    int rc = launch_stage(k, s, ex.ptrs.data(), k->ws, ex.stream);
     if (rc) return rc;
   }
   if (ex.is_padded) {
@@ -792,7 +795,75 @@ static int launch_impl(tf_kernel_t *k, void *const *device_buffers, void *stream
   int rc = pointer_table(k, device_buffers, ptrs);
   if (rc) return rc;
   for (size_t s = 0; s < k->plan.stages.size(); ++s) {
-    rc = launch_stage(k, s, ptrs.data(), static_cast<hipStream_t>(stream));
+    rc = launch_stage(k, s, ptrs.data(), k->ws, static_cast<hipStream_t>(stream));
+    if (rc) return rc;
+  }
+  return TF_OK;
+}
+
+// ------------------------------------------------ allocation-free launch ---
+//
+// tf_launch_noalloc takes the split-K workspace and the intermediates of
+// multi-launch programs from `scratch`, one fixed array per GPU, instead of
+// the handle's hipMalloc'd buffers.  The array's host-side name is only a
+// stand-in: its device address, which differs per GPU, is fetched once per
+// device with hipGetSymbolAddress and kept in g_scratch.
+constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+struct ScratchSlot {
+  std::once_flag once;
+  void *ptr = nullptr;
+  hipError_t err = hipSuccess;
+};
+static ScratchSlot g_scratch[kMaxDevices];
+
+// Device address of the current device's scratch array.
+static int scratch_base(void **out) {
+  int dev = 0;
+  TF_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return fail(TF_E_ARG, "device " + std::to_string(dev) + " out of range");
+  ScratchSlot &slot = g_scratch[dev];
+  std::call_once(slot.once, [&] { slot.err = hipGetSymbolAddress(&slot.ptr, HIP_SYMBOL(scratch)); });
+  if (slot.err != hipSuccess)
+    return fail(TF_E_HIP, std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(slot.err));
+  *out = slot.ptr;
+  return TF_OK;
+}
+
+static int launch_noalloc_impl(tf_kernel_t *k, void *const *device_buffers, void *stream) {
+  if (!k || !device_buffers) return fail(TF_E_ARG, "null kernel or buffers");
+  int rc = check_buffers(k, device_buffers);
+  if (rc) return rc;
+  // Scratch layout: the split-K workspace, then each intermediate, each
+  // starting on a 256-byte boundary.  Nothing needs clearing: every split
+  // writes its whole slice before the reduction reads it, and every
+  // intermediate is written whole by the launch that produces it.
+  const tff::Plan &pl = k->plan;
+  size_t used = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = used;
+    used += (bytes + 255) / 256 * 256;
+    return at;
+  };
+  const size_t ws_at = k->ws_bytes ? take(k->ws_bytes) : 0;
+  std::vector<size_t> at(pl.buffers.size(), 0);
+  for (size_t i = pl.nargs + 1; i < pl.buffers.size(); ++i)
+    at[i] = take(std::max<int64_t>(1, pl.buffers[i].numel()) * sizeof(float));
+  if (used > kScratchBytes)
+    return fail(TF_E_ARG, "this program needs " + std::to_string(used) + " bytes of scratch (split-K workspace and "
+                          "intermediates); tf_launch_noalloc has " + std::to_string(kScratchBytes) +
+                          " per GPU: use tf_launch, which allocates them");
+  void *base = nullptr;
+  rc = scratch_base(&base);
+  if (rc) return rc;
+  std::vector<void *> ptrs(pl.buffers.size(), nullptr);
+  for (int i = 0; i <= pl.nargs; ++i) ptrs[i] = device_buffers[i];
+  for (size_t i = pl.nargs + 1; i < pl.buffers.size(); ++i) ptrs[i] = static_cast<unsigned char *>(base) + at[i];
+  void *ws = k->ws_bytes ? static_cast<unsigned char *>(base) + ws_at : nullptr;
+  for (size_t s = 0; s < pl.stages.size(); ++s) {
+    rc = launch_stage(k, s, ptrs.data(), ws, static_cast<hipStream_t>(stream));
     if (rc) return rc;
   }
   return TF_OK;
@@ -936,6 +1007,10 @@ int tf_compile(const char *source_name, const char *program, const char *options
 
 int tf_launch(tf_kernel_t *k, void *const *device_buffers, void *stream) {
   return guarded([&] { return launch_impl(k, device_buffers, stream); });
+}
+
+int tf_launch_noalloc(tf_kernel_t *k, void *const *device_buffers, void *stream) {
+  return guarded([&] { return launch_noalloc_impl(k, device_buffers, stream); });
 }
 
 int tf_run(tf_kernel_t *k, int mode, const long long *logical_mnk, const float *const *host_inputs, float *host_out) {
