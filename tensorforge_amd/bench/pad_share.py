@@ -29,6 +29,7 @@ from tensorforge_amd import costmodel as cm
 from tensorforge_amd import provenance
 from tensorforge_amd import tforge_cpu as tc
 from tensorforge_amd import tforge_gpu as tg
+from tensorforge_amd.bench import harness
 
 SHAPES = [(1000, 1000, 1000), (777, 1111, 333), (3000, 2000, 1000), (4095, 4097, 1023)]
 REFERENCE = "block-tile=128,64 thread-tile=8,4 tile-k=16 promote=1 vectorize=1"  # docs/stage8.md:107
@@ -46,8 +47,8 @@ def main(argv=None):
     shapes = SHAPES
     if args.shapes:
         shapes = [tuple(int(v) for v in s.split("x")) for s in args.shapes.split(",")]
-    base = provenance.common()
-    out = provenance.CsvWriter(args.csv)
+    out = provenance.ResultsTable(args.csv, device=harness.device_label(), dtype="f32", threads="",
+                                  alloc_bytes_per_call="", clock_adjusted_metric="")
     wl = args.workload
     failures = 0
     for m, n, k in shapes:
@@ -75,16 +76,13 @@ def main(argv=None):
             t_kern = padded.bench(warmup=args.warmup, reps=args.reps)
             t_mask = masked.bench(warmup=args.warmup, reps=args.reps)
             share = 1.0 - t_kern.median_ms / t_path.median_ms
-            dev = _lib.device_info()
             for label, r, pipe in (("pad_path", t_path, opts), ("padded_kernel", t_kern, opts),
                                    ("masked", t_mask, opts + " mask-edges=1")):
                 gf = flops / (r.median_ms * 1e-3) / 1e9
-                out.row(**base, device=dev["name"] or dev["arch"], workload=wl, shape=f"{m}x{n}x{k}", dtype="f32",
-                        pipeline=f"tforge-gpu-pipeline{{{pipe}}}",
-                        params=f"{name}; {label}; padded={pm}x{pn}x{pk}", threads="", warmup=args.warmup,
+                out.add(workload=wl, shape=f"{m}x{n}x{k}", pipeline=f"tforge-gpu-pipeline{{{pipe}}}",
+                        params=f"{name}; {label}; padded={pm}x{pn}x{pk}", warmup=args.warmup,
                         reps=args.reps, median_ms=r.median_ms, min_ms=r.min_ms, std_ms=r.std_ms,
                         metric="GFLOP/s (logical shape)", metric_value=gf, sm_clock_median_mhz=r.clock_median_mhz,
-                        clock_adjusted_metric="", alloc_bytes_per_call="",
                         correctness=f"err/bound={chk['err_over_bound']:.3g}; masked vs pad path bitwise diffs={same}",
                         notes=(f"pad_share={share:.3f}; masked speedup over pad path="
                                f"{t_path.median_ms / t_mask.median_ms:.3f}"))

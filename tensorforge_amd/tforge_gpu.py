@@ -129,18 +129,27 @@ def info(workload, m, n, k, kdir, launch):
     return _kernel(kdir, launch).resources(0)
 
 
-def _bound_check(workload, ins, out, k):
-    """The reference's FP64 check (python/tforge_gpu.py:134-145), plus the
-    ReLU mask rule: where |pre-activation| > bound, out == 0 iff z <= 0."""
+def reference64(workload, ins):
+    """FP64 reference of a matmul or mbr on its inputs (python/tforge_gpu.py:134-145):
+    (ref, bound, z) with ref = A64 @ B64 (+ bias64, max 0), bound =
+    gamma_j * (|A64| @ |B64| (+ |bias64|)) + FLT_MIN, gamma_j = j u / (1 - j u),
+    u = 2^-24, j = K (+1 for mbr), and z the FP64 pre-activation whose sign
+    the ReLU decides (None for matmul)."""
     a64, b64 = ins["a"].astype(np.float64), ins["b"].astype(np.float64)
-    ref, mag, steps = a64 @ b64, np.abs(a64) @ np.abs(b64), k
+    acc, mag, steps = a64 @ b64, np.abs(a64) @ np.abs(b64), a64.shape[1]
     z = None
     if workload == "mbr":
         bias64 = ins["bias"].astype(np.float64)
-        z = ref + bias64
-        ref, mag, steps = np.maximum(z, 0.0), mag + np.abs(bias64), k + 1
+        z = acc + bias64
+        acc, mag, steps = np.maximum(z, 0.0), mag + np.abs(bias64), steps + 1
     gamma = steps * tc.F32_EPS / (1 - steps * tc.F32_EPS)
-    bound = gamma * mag + np.finfo(np.float32).tiny
+    return acc, gamma * mag + np.finfo(np.float32).tiny, z
+
+
+def bound_verdict(out, ref, bound, z=None):
+    """The reference's pass rule on an output: no NaN (outputs are
+    NaN-prefilled) and err/bound <= 1; plus, where z is given, the ReLU mask
+    rule: where |z| > bound, out == 0 exactly when z <= 0."""
     err = np.abs(out.astype(np.float64) - ref)
     res = {"nan_count": int(np.isnan(out).sum()),
            "max_abs_err": float(np.nanmax(err)) if err.size else 0.0,
@@ -150,6 +159,22 @@ def _bound_check(workload, ins, out, k):
         res["mask_mismatches"] = int(np.count_nonzero(decided & ((out == 0) != (z <= 0))))
     res["pass"] = res["nan_count"] == 0 and res["err_over_bound"] <= 1.0 and res.get("mask_mismatches", 0) == 0
     return res
+
+
+def elementwise_verdict(workload, ins, out):
+    """Element ops must equal NumPy float32 bit for bit (python/tforge_gpu.py:116-126)."""
+    with np.errstate(invalid="ignore", over="ignore"):
+        want = {"bias_add": lambda: ins["a"] + ins["bias"], "add": lambda: ins["a"] + ins["b"],
+                "relu": lambda: np.maximum(ins["a"], np.float32(0))}[workload]()
+    want = np.ascontiguousarray(want, np.float32)
+    exact = bool(np.array_equal(out.view(np.uint32), want.view(np.uint32)))
+    return {"pass": exact, "nan_count": int(np.isnan(out).sum()), "err_over_bound": 0.0 if exact else float("inf"),
+            "max_abs_err": float(np.max(np.abs(out.astype(np.float64) - want))) if out.size else 0.0}
+
+
+def _bound_check(workload, ins, out, k):
+    """reference64 + bound_verdict for a matmul or mbr output."""
+    return bound_verdict(out, *reference64(workload, ins))
 
 
 def _resmlp_check(ins, out):
@@ -176,33 +201,33 @@ def _resmlp_check(ins, out):
     return res
 
 
-def check(workload, m, n, k, kdir=None, launch=None, mode="kernel", seed=1234):
-    """Run once on seeded inputs and check (python/tforge_gpu.py:112-145): the
-    FP64 bound for matmul / mbr (and its two-layer composition for resmlp);
-    elementwise workloads must match NumPy float32 exactly.  Returns
-    (result dict, output)."""
-    ins = tc.make_inputs(workload, m, n, k, seed)
-    arrays = [np.ascontiguousarray(v) for v in ins.values()]
+def execute(workload, m, n, k, arrays, kdir=None, launch=None, mode="kernel"):
+    """One correctness run (NaN-prefilled output) of a compiled kernel, or of
+    the vendor-library mode, on host arrays in entry-argument order."""
     out = np.empty((m, n), dtype=np.float32)
     if mode == "kernel":
-        kern = _kernel(kdir, launch)
-        kern.run(arrays, out, _lib.TF_MODE_KERNEL, _logical(workload, m, n, k, launch))
+        _kernel(kdir, launch).run(arrays, out, _lib.TF_MODE_KERNEL, _logical(workload, m, n, k, launch))
     else:
         _blas_kernel(workload, m, n, k).run(arrays, out, _mode(mode))
+    return out
+
+
+def verdict(workload, ins, out):
+    """Pass/fail of an output for its workload: bit-exact element ops, the
+    FP64 bound for matmul / mbr, its two-layer composition for resmlp."""
     if workload in ("bias_add", "relu", "add"):
-        if workload == "bias_add":
-            ref = ins["a"] + ins["bias"]
-        elif workload == "add":
-            ref = ins["a"] + ins["b"]
-        else:
-            ref = np.maximum(ins["a"], np.float32(0))
-        exact = bool(np.array_equal(out.view(np.uint32), np.ascontiguousarray(ref, np.float32).view(np.uint32)))
-        return {"pass": exact, "nan_count": int(np.isnan(out).sum()),
-                "err_over_bound": 0.0 if exact else float("inf"),
-                "max_abs_err": float(np.max(np.abs(out.astype(np.float64) - ref))) if out.size else 0.0}, out
+        return elementwise_verdict(workload, ins, out)
     if workload == "resmlp":
-        return _resmlp_check(ins, out), out
-    return _bound_check(workload, ins, out, k), out
+        return _resmlp_check(ins, out)
+    return bound_verdict(out, *reference64(workload, ins))
+
+
+def check(workload, m, n, k, kdir=None, launch=None, mode="kernel", seed=1234):
+    """Run once on seeded inputs and check (python/tforge_gpu.py:112-145).
+    Returns (result dict, output)."""
+    ins = tc.make_inputs(workload, m, n, k, seed)
+    out = execute(workload, m, n, k, [np.ascontiguousarray(v) for v in ins.values()], kdir, launch, mode)
+    return verdict(workload, ins, out), out
 
 
 def bench(workload, m, n, k, kdir=None, launch=None, mode="kernel", warmup=10, reps=100, flush=False):
