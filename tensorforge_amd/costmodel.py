@@ -98,7 +98,8 @@ def _block(tm, tn):
 
 def _lds_bytes(bm, bn, tm, tn, bk):
     # two A and B tile buffers plus the tile's bias values
-    return (2 * (bm * (bk + 4) + bk * (bn + (8 if _block(tm, tn) == 32 else 4))) + bn) * 4
+    mb = _block(tm, tn)
+    return (2 * (bm * (bk + (4 if mb == 32 else 8)) + bk * (bn + (8 if mb == 32 else 4))) + bn) * 4
 
 
 def reference_space():

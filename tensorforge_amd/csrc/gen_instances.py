@@ -42,7 +42,7 @@ def staged_valid(bm, bn, tm, tn, bk, promote=1):
     mb = 32 if wtm % 32 == 0 and wtn % 32 == 0 else 16
     if bk % (256 // mb):
         return f"tile-k must be a multiple of {256 // mb} for {mb}x{mb} MFMA blocks"
-    lds = (2 * (bm * (bk + 4) + bk * (bn + (8 if mb == 32 else 4))) + bn) * 4 if promote else 0
+    lds = (2 * (bm * (bk + (4 if mb == 32 else 8)) + bk * (bn + (8 if mb == 32 else 4))) + bn) * 4 if promote else 0
     if lds > LDS_LIMIT:
         return f"LDS {lds} B exceeds 160 KiB"
     return None

@@ -75,7 +75,7 @@ std::string staged_reason(long bm, long bn, long tm, long tn, long bk, bool prom
   if (bk % kc)
     return "tile-k must be a multiple of " + std::to_string(kc) + " for " + std::to_string(mb) + "x" +
            std::to_string(mb) + " MFMA blocks";
-  const long lds = promote ? 2 * (bm * (bk + 4) + bk * (bn + (mb == 32 ? 8 : 4))) * 4 : 0;
+  const long lds = promote ? 2 * (bm * (bk + (mb == 32 ? 4 : 8)) + bk * (bn + (mb == 32 ? 8 : 4))) * 4 : 0;
   if (lds > 160 * 1024) return "LDS " + std::to_string(lds) + " B exceeds 160 KiB";
   return "no ahead-of-time instantiation of this configuration in libtforge_hip";
 }

@@ -20,7 +20,7 @@
 //    one column.  The sum order differs from the reference's sequential k;
 //    parity is the reference's own FP64 error bound, which holds for any
 //    order (python/tforge_cpu.py:263-271).
-//  * Staging (promote=1).  A tile [BM][BK+4] and B tile [BK][BN+8] in LDS,
+//  * Staging (promote=1).  A tile [BM][BK+4 or +8] and B tile [BK][BN+8 or +4] in LDS,
 //    double-buffered, one barrier per slab.  Two register staging sets where
 //    a thread stages few vectors: the global loads of slab t+3 are issued in
 //    the middle of slab t, two slabs before they are written to LDS (in the
@@ -104,7 +104,11 @@ struct StagedGemm {
   static constexpr int MB = (WTM % 32 == 0 && WTN % 32 == 0) ? 32 : 16;  // MFMA block
   static constexpr int KC = 256 / MB;                                     // k per chunk
   static constexpr int FM = WTM / MB, FN = WTN / MB;
-  static constexpr int LDA = BK + 4;  // LDS A row stride (floats): odd multiple of 4
+  // LDS A row stride (floats).  A fragment read (ds_read_b128) has lanes
+  // (lr, lg) at lr * LDA + 4 * lg: conflict-free for MB = 32 with BK + 4, and
+  // for MB = 16 (4 lane groups on one row) only with LDA = 8 mod 16, so BK + 8
+  // (measured on gfx950: BK + 4 costs 4 bank-conflict cycles per read).
+  static constexpr int LDA = BK + ((WTM % 32 == 0 && WTN % 32 == 0) ? 4 : 8);
   // LDS B row stride: the 64 / MB lane groups read rows 4 apart; +8 (MB = 32)
   // or +4 (MB = 16) puts them in disjoint banks.
   static constexpr int LDB = BN + (MB == 32 ? 8 : 4);
