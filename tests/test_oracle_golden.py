@@ -76,6 +76,15 @@ def test_stage8_err_over_bound(key):
     assert sig(o.e1_metrics(out, ref, bound)["max_err_over_bound"], digits) == float(want)
 
 
+@pytest.mark.slow
+@pytest.mark.parametrize("key", sorted(k for k in STAGE8 if max(shape_of(k)[1:]) > 2048))
+def test_stage8_err_over_bound_4096(key):
+    """The 4096^3 rows of the same column (results/gpu/stage8.csv): the FMA
+    closed form on all host cores (its bits do not depend on the thread
+    count), FP64 reference from NumPy."""
+    test_stage8_err_over_bound(key)
+
+
 @pytest.mark.parametrize("key", sorted(CPU))
 def test_cpu_pipeline_err_over_bound(key):
     """results/cpu/stage4.csv, stage6_best.csv: the reference's default scalar
