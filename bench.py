@@ -18,10 +18,13 @@ A step is one launch of the compiled program over device-resident inputs
   3. the shader clock measured on the device right after the window
      (tf_clock_probe: s_memtime cycles against the 100 MHz wall clock, one
      workgroup per XCD);
-  4. K more launches, each bracketed by its own event pair on the same stream:
-     their average is the kernel duration behind `roofline.achieved` and their
-     median is reported beside it, as the reference runner reports the median
-     (runners/gpu/tforge-gpu-bench.cu:345-363).
+  4. K more launches, each bracketed by its own event pair on the same stream;
+     their average and median (the reference runner reports medians,
+     runners/gpu/tforge-gpu-bench.cu:345-363) go into the line beside the
+     window's.  `roofline.achieved` uses the window: the average launch
+     duration over the timed region.  A launch alone between its own events
+     also pays its dispatch and completion latency (3-12 us more, varying
+     between machines), which back-to-back launches overlap.
 
 TFLOP/s = 2*M*N*K / time (the reference's convention, bench/gpu_bench.py:57);
 the peak is MI355X's published FP32 matrix figure, 157.3 TFLOP/s.  The
@@ -335,7 +338,7 @@ def main():
     value = flops / (window_ms * 1e-3) / 1e12
     avg_ms = statistics.fmean(per_launch)
     med_ms = statistics.median(per_launch)
-    achieved = flops / (avg_ms * 1e-3) / 1e12
+    achieved = flops / (window_ms * 1e-3) / 1e12
     log(f"{launch['kernel']}: {window_ms * 1e3:.1f} us/step, {value:.2f} TFLOP/s, per-launch avg "
         f"{avg_ms * 1e3:.1f} / median {med_ms * 1e3:.1f} us, clock {clock_mhz[0]:.0f} MHz, parity {parity}")
 
@@ -379,7 +382,9 @@ def main():
                      "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": traffic,
                      "traffic_source": "profiles/traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)"
                      if traffic else None,
-                     "kernel_avg_ms": avg_ms, "kernel_median_ms": med_ms, "flop_per_launch": flops},
+                     "kernel_avg_ms": window_ms, "flop_per_launch": flops,
+                     "per_launch_events": {"avg_ms": avg_ms, "median_ms": med_ms,
+                                           "note": "each launch between its own event pair, after the window"}},
         "parity": parity, "autotune": autotune, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
