@@ -43,7 +43,8 @@ def _units():
     sys.path.insert(0, str(CSRC))
     import gen_instances  # noqa: E402
     gen_instances.main()
-    units = [CSRC / "runtime.hip", CSRC / "direct_kernels.hip", CSRC / "_gen" / "registry.hip"]
+    units = [CSRC / "runtime.hip", CSRC / "direct_kernels.hip", CSRC / "_gen" / "registry.hip",
+             CSRC / "_gen" / "streamed.hip"]
     units += sorted((CSRC / "_gen").glob("staged_*.hip"))
     return units
 
@@ -80,6 +81,10 @@ def _entry_name(demangled):
         bm, bn, tm, tn, bk, p, v, mk = m.groups()
         return (f"tf_staged_b{bm}x{bn}_t{tm}x{tn}_k{bk}" + ("" if p == "1" else "_noprom") +
                 ("" if v == "1" else "_novec") + ("_masked" if mk == "1" else ""))
+    m = re.search(r"streamed_gemm_kernel<(\d+), (\d+), (\d+), (\d+), (\d+)>", demangled)
+    if m:
+        bm, bn, tm, tn, bk = m.groups()
+        return f"tf_streamed_b{bm}x{bn}_t{tm}x{tn}_k{bk}"
     m = re.search(r"(direct_gemm|elementwise)_kernel<(\d+), (\d+)>", demangled)
     if m:
         fam = "direct" if m.group(1) == "direct_gemm" else "elementwise"

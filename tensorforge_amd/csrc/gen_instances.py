@@ -77,6 +77,23 @@ def configs():
 
 MASK_MAX_VECTORS = 16
 
+# Streamed (persistent) instantiations: the configurations that win on
+# problems with many tiles, whose LDS (A/B buffers, bias, and a whole C tile)
+# fits in 160 KiB.
+STREAMED = [(128, 128, 8, 4, 16), (128, 128, 8, 4, 32), (128, 128, 4, 4, 32), (128, 128, 8, 8, 32),
+            (64, 128, 4, 4, 32), (128, 64, 4, 4, 32), (64, 64, 4, 4, 32), (64, 128, 4, 4, 64),
+            (64, 64, 4, 2, 64), (64, 64, 2, 2, 64)]
+
+
+def streamed_lds(bm, bn, tm, tn, bk):
+    mb = 32 if (8 * tm) % 32 == 0 and (8 * tn) % 32 == 0 else 16
+    return (2 * (bm * (bk + (4 if mb == 32 else 8)) + bk * (bn + (8 if mb == 32 else 4))) + bn + bm * (bn + 4)) * 4
+
+
+def streamed_name(c):
+    bm, bn, tm, tn, bk = c
+    return f"tf_streamed_b{bm}x{bn}_t{tm}x{tn}_k{bk}"
+
 
 def staging_vectors(bm, bn, tm, tn, bk, vec=1):
     """Global-load vectors (128-bit, or 32-bit without vectorize) a thread stages per slab."""
@@ -115,8 +132,26 @@ def main(shards=16):
         p = gen / f"staged_{i:02d}.hip"
         if not p.exists() or p.read_text() != text:
             p.write_text(text)
+    lines = ['#include "../streamed_gemm.hpp"', "", "namespace tfk {", "",
+             "#ifndef __HIP_DEVICE_COMPILE__  // host registry data", "extern const KernelEntry kStreamed[] = {"]
+    for c in STREAMED:
+        assert staged_valid(*c) is None and streamed_lds(*c) <= LDS_LIMIT, c
+        t = ", ".join(str(x) for x in c)
+        lines.append(f"    KernelEntry{{FAM_STREAMED, {t}, 1, 1, 0, \"{streamed_name(c)}\",")
+        lines.append(f"                reinterpret_cast<const void *>(&streamed_gemm_kernel<{t}>),")
+        lines.append(f"                &launch_streamed<{t}>, nullptr, StreamedGemm<{t}>::LDS_BYTES}},")
+    lines += ["};", f"extern const int kStreamedCount = {len(STREAMED)};", "#else",
+              "// Device pass: instantiate the kernels the host table names."]
+    for c in STREAMED:
+        lines.append(f"template __global__ void streamed_gemm_kernel<{', '.join(str(x) for x in c)}>(GemmParams);")
+    lines += ["#endif", "", "}  // namespace tfk", ""]
+    text = "\n".join(lines)
+    p = gen / "streamed.hip"
+    if not p.exists() or p.read_text() != text:
+        p.write_text(text)
     reg = ['#include <vector>', '', '#include "../tf_kernels.h"', '', 'namespace tfk {', '',
-           'extern const KernelEntry kDirectEntries[];', 'extern const int kDirectCount;']
+           'extern const KernelEntry kDirectEntries[];', 'extern const int kDirectCount;',
+           'extern const KernelEntry kStreamed[];', 'extern const int kStreamedCount;']
     for i in range(shards):
         reg += [f"extern const KernelEntry kStaged{i}[];", f"extern const int kStagedCount{i};"]
     reg += ["", "static const std::vector<KernelEntry> &all_entries() {",
@@ -124,7 +159,8 @@ def main(shards=16):
             "    std::vector<KernelEntry> r(kDirectEntries, kDirectEntries + kDirectCount);"]
     for i in range(shards):
         reg.append(f"    r.insert(r.end(), kStaged{i}, kStaged{i} + kStagedCount{i});")
-    reg += ["    return r;", "  }();", "  return v;", "}", "",
+    reg += ["    r.insert(r.end(), kStreamed, kStreamed + kStreamedCount);",
+            "    return r;", "  }();", "  return v;", "}", "",
             "const KernelEntry *registry_begin() { return all_entries().data(); }",
             "const KernelEntry *registry_end() { return all_entries().data() + all_entries().size(); }",
             "", "}  // namespace tfk", ""]
@@ -132,7 +168,7 @@ def main(shards=16):
     p = gen / "registry.hip"
     if not p.exists() or p.read_text() != text:
         p.write_text(text)
-    print(f"{len(cfgs)} staged instantiations in {shards} shards")
+    print(f"{len(cfgs)} staged instantiations in {shards} shards, {len(STREAMED)} streamed")
 
 
 if __name__ == "__main__":

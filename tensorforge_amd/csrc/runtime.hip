@@ -130,8 +130,28 @@ int select_launches(tf_kernel *k) {
       return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc,
                                                 "tforge-gpu-pipeline: mask-edges supports matrices below 2^31 "
                                                 "elements; pad this problem instead"));
+    // persistent: the streamed kernel for GEMM stages (element-op launches of
+    // an unfused program run as they are).
+    const bool streamed = o.persistent && gemm;
+    if (streamed) {
+      std::string why;
+      if (!staged) why = "persistent needs tile-k";
+      else if (masked) why = "persistent needs M, N and K to be multiples of the block and K tiles (pad the problem)";
+      else if (o.split_k > 1) why = "persistent and split-k exclude each other";
+      else if (!o.promote || !o.vectorize) why = "persistent needs promote=1 vectorize=1";
+      else if (st.K < 4 * o.tile_k || (st.K / o.tile_k) % 2) why = "persistent needs K to be an even number (at least 4) of tile-k slabs";
+      // The streamed kernel's per-thread staging offsets are 32-bit.
+      else if (o.bm * st.K >= (1L << 31) || o.tile_k * st.N >= (1L << 31)) why = "persistent supports BM*K and BK*N below 2^31";
+      if (!why.empty()) return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc, "tforge-gpu-pipeline: " + why));
+    }
     for (const tfk::KernelEntry *e = tfk::registry_begin(); e != tfk::registry_end(); ++e) {
-      if (staged) {
+      if (streamed) {
+        if (e->family == tfk::FAM_STREAMED && e->bm == o.bm && e->bn == o.bn && e->tm == o.tm && e->tn == o.tn &&
+            e->bk == o.tile_k) {
+          L.entry = e;
+          break;
+        }
+      } else if (staged) {
         if (e->family == tfk::FAM_STAGED && e->bm == o.bm && e->bn == o.bn && e->tm == o.tm && e->tn == o.tn &&
             e->bk == o.tile_k && e->promote == (int)o.promote && e->vectorize == (int)o.vectorize &&
             e->masked == masked) {
@@ -157,6 +177,11 @@ int select_launches(tf_kernel *k) {
                                                       " vectors per slab (at most 16); use more threads or a smaller "
                                                       "tile-k, or pad the problem"));
     }
+    if (!L.entry && streamed)
+      return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc,
+                                                "tforge-gpu-pipeline: persistent has no instantiation of this "
+                                                "configuration (" + staged_reason(o.bm, o.bn, o.tm, o.tn, o.tile_k, true) +
+                                                "); streamed configurations are listed by tf_registry_entry"));
     if (!L.entry) {
       std::string why = staged ? staged_reason(o.bm, o.bn, o.tm, o.tn, o.tile_k, o.promote)
                                : "thread-tile " + std::to_string(o.tm) + "," + std::to_string(o.tn) +
@@ -170,6 +195,7 @@ int select_launches(tf_kernel *k) {
                                                     " threads per block exceeds 1024"));
     L.block = dim3((unsigned)tx, (unsigned)ty, 1);
     L.grid = dim3((unsigned)std::max(1L, ceil_div(st.N, o.bn)), (unsigned)std::max(1L, ceil_div(st.M, o.bm)), 1);
+    if (streamed) L.grid = dim3((unsigned)std::min<long>(tfk::kStreamedGrid, (long)L.grid.x * L.grid.y), 1, 1);
     // split-k splits the K loop of GEMM stages; the element-op launches of an
     // unfused program run as they are.  Without tile-k it is an error.
     if (o.split_k > 1 && (gemm || o.tile_k == 0)) {
@@ -210,7 +236,7 @@ int launch_stage(const tf_kernel *k, size_t s, void *const *ptrs, void *ws, hipS
   if (st.M == 0 || st.N == 0) return TF_OK;
   // 128-bit accesses need 16-byte aligned buffers (the reference's ABI
   // guarantees 256-byte alignment: docs/stage8.md:34).
-  if (L.entry->family == tfk::FAM_STAGED) {
+  if (L.entry->family == tfk::FAM_STAGED || L.entry->family == tfk::FAM_STREAMED) {
     std::vector<int> ids = {st.a, st.b, st.out};
     for (const tff::EpiOp &e : st.epi)
       if (e.buf >= 0) ids.push_back(e.buf);

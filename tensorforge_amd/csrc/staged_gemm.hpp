@@ -73,8 +73,11 @@ __device__ __forceinline__ AccOf<MB> mfma_block(float b, float a, AccOf<MB> c) {
   else return __builtin_amdgcn_mfma_f32_16x16x4f32(b, a, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ void staged_tile_coords(int gx, int gy, int swizzle, int &tm, int &tn) {
-  int w = blockIdx.y * gx + blockIdx.x;
+// Output tile (tm, tn) of linear tile index w on a gx x gy tile grid.  With
+// swizzle, consecutive w are dealt to the 8 XCDs round-robin (as the hardware
+// deals workgroups), so the indices one XCD receives are remapped to a
+// compact block of tiles, grouped by 4 tile rows.
+__device__ __forceinline__ void tile_coords(int w, int gx, int gy, int swizzle, int &tm, int &tn) {
   const int total = gx * gy;
   if (!swizzle) {
     tm = w / gx;
@@ -90,6 +93,10 @@ __device__ __forceinline__ void staged_tile_coords(int gx, int gy, int swizzle, 
   const int r = w - group * kGroup * gx;
   tm = first + r % rows;
   tn = r / rows;
+}
+
+__device__ __forceinline__ void staged_tile_coords(int gx, int gy, int swizzle, int &tm, int &tn) {
+  tile_coords(blockIdx.y * gx + blockIdx.x, gx, gy, swizzle, tm, tn);
 }
 
 // Write element e of a staging register (a float or a 4-vector).

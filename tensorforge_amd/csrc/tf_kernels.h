@@ -65,7 +65,11 @@ struct EltParams {
   int vec_ok;  // 1: every operand 16-byte aligned with row strides a multiple of 4
 };
 
-enum Family : int { FAM_DIRECT = 0, FAM_STAGED = 1, FAM_ELEMENTWISE = 2 };
+enum Family : int { FAM_DIRECT = 0, FAM_STAGED = 1, FAM_ELEMENTWISE = 2, FAM_STREAMED = 3 };
+
+// Workgroups of a streamed (persistent) launch: one per MI355X compute unit,
+// or one per tile when there are fewer tiles.
+constexpr int kStreamedGrid = 256;
 
 using GemmLauncher = hipError_t (*)(const GemmParams &, dim3 grid, dim3 block, hipStream_t);
 using EltLauncher = hipError_t (*)(const EltParams &, dim3 grid, dim3 block, hipStream_t);

@@ -235,3 +235,35 @@ def test_null_device_pointer_is_refused_before_any_launch():
     out = np.zeros((64, 64), np.float32)
     assert L.tf_run(k.h, 0, None, ins, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))) == -4
     assert b"host input 0 is a null pointer" in L.tf_last_error()
+
+
+@pytest.mark.parametrize("shape,options,message", [
+    ((1000, 1024, 256), STAGED_16 + " mask-edges=1 persistent=1", "persistent needs M, N and K to be multiples"),
+    ((1024, 1024, 256), STAGED_16 + " split-k=2 persistent=1", "persistent and split-k exclude each other"),
+    ((1024, 1024, 256), "block-tile=16,16 thread-tile=1,1 persistent=1", "persistent needs tile-k"),
+    ((1024, 1024, 32), "block-tile=128,128 thread-tile=8,4 tile-k=16 promote=1 vectorize=1 persistent=1",
+     "persistent needs K to be an even number"),
+    ((1024, 1024, 160), "block-tile=128,128 thread-tile=8,4 tile-k=32 promote=1 vectorize=1 persistent=1",
+     "persistent needs K to be an even number"),
+    ((1024, 1024, 256), "block-tile=128,128 thread-tile=8,4 tile-k=32 promote=0 vectorize=1 persistent=1",
+     "persistent needs promote=1 vectorize=1"),
+    ((1024, 1024, 256), "block-tile=128,256 thread-tile=8,4 tile-k=32 promote=1 vectorize=1 persistent=1",
+     "persistent has no instantiation of this configuration"),
+])
+def test_persistent_option_refusals(shape, options, message):
+    """The persistent (streamed) option's limits are compile-time errors with
+    the reason (no GPU needed)."""
+    from tensorforge_amd import _lib
+    with pytest.raises(RuntimeError, match=message):
+        _lib.Kernel(tc.gen_mlir("mbr", *shape), options)
+
+
+def test_persistent_launch_geometry():
+    """One workgroup per compute unit (256), or one per tile when fewer."""
+    from tensorforge_amd import _lib
+    opts = "block-tile=128,128 thread-tile=8,4 tile-k=32 promote=1 vectorize=1 persistent=1"
+    big = _lib.Kernel(tc.gen_mlir("mbr", 4096, 4096, 256), opts).launches()[0]
+    assert big["family"] == "streamed" and big["grid"] == [256, 1, 1] and big["block"] == [32, 16, 1]
+    assert big["kernel"] == "tf_streamed_b128x128_t8x4_k32"
+    small = _lib.Kernel(tc.gen_mlir("mbr", 1024, 1024, 256), opts).launches()[0]
+    assert small["grid"] == [64, 1, 1]
