@@ -113,3 +113,61 @@ def test_full_size_residual_block():
     sub = dict(host)
     sub["x"] = host["x"][rows]
     assert tg._resmlp_check(sub, y[rows].cpu().numpy())["pass"]
+
+
+# Layer 2 of the residual block as a program of its own: relu(h @ w2 + b2) + x.
+LAYER2 = """func.func @entry(%h: {h}, %w2: {w2}, %b2: {b2}, %x: {y}) -> {y} {{
+  %0 = tforge.matmul %h, %w2 : {h}, {w2} -> {y}
+  %1 = tforge.bias_add %0, %b2 : {y}, {b2} -> {y}
+  %2 = tforge.relu %1 : {y} -> {y}
+  %3 = tforge.add %2, %x : {y}, {y} -> {y}
+  return %3 : {y}
+}}
+"""
+
+
+def test_full_size_residual_layers_against_the_oracle():
+    """The residual block at its benchmark size, one layer at a time against
+    the oracle.  Layer 1, relu(x @ w1 + b1), runs as its own program with the
+    block's configuration and meets the reference bound with exact ReLU masks
+    on sampled rows.  Layer 2 on the kernel's own float32 h meets the reference
+    bound widened by the final add's one rounding, u (|relu(z) + x| + bound),
+    and where the ReLU decides zero the output is x itself, bit for bit.  The
+    block equals the two programs run one after the other, bit for bit, so
+    the two checks cover it."""
+    torch, dev = _torch()
+    m, n, k = 4096, 2048, 8192
+    opts = "block-tile=128,256 thread-tile=8,4 tile-k=32 promote=1 vectorize=1"
+    stream = torch.cuda.current_stream().cuda_stream
+    host = tc.make_inputs("resmlp", m, n, k)
+    x, w1, b1, w2, b2 = (torch.from_numpy(np.ascontiguousarray(host[s])).to(dev) for s in ("x", "w1", "b1", "w2", "b2"))
+
+    def run(program, args, shape):
+        out = torch.full(shape, float("nan"), device=dev)
+        _lib.Kernel(program, opts, "t.mlir").launch([a.data_ptr() for a in args] + [out.data_ptr()], stream)
+        torch.cuda.synchronize()
+        return out
+
+    t = lambda *s: "tensor<" + "x".join(map(str, s)) + "xf32>"
+    h = run(tc.gen_mlir("mbr", m, k, n), [x, w1, b1], (m, k))
+    y2 = run(LAYER2.format(h=t(m, k), w2=t(k, n), b2=t(n), y=t(m, n)), [h, w2, b2, x], (m, n))
+    y = run(tc.gen_mlir("resmlp", m, n, k), [x, w1, b1, w2, b2], (m, n))
+    assert torch.equal(_bits(y), _bits(y2))
+
+    rows = np.sort(np.random.default_rng(11).choice(m, size=32, replace=False))
+    layer1 = {"a": host["x"][rows], "b": host["w1"], "bias": host["b1"]}
+    ref1, bound1 = o.fp64_reference("mbr", layer1)
+    h_rows = h[rows].cpu().numpy()
+    assert o.e1_metrics(h_rows, ref1, bound1)["max_err_over_bound"] <= 1.0
+    assert o.mask_mismatches(h_rows, o.preactivation64(layer1), bound1) == 0
+
+    layer2 = {"a": h_rows, "b": host["w2"], "bias": host["b2"]}
+    ref2, bound2 = o.fp64_reference("mbr", layer2)
+    x_rows = host["x"][rows]
+    y_ref = ref2 + x_rows.astype(np.float64)
+    y_rows = y[rows].cpu().numpy()
+    assert o.e1_metrics(y_rows, y_ref, bound2 + o.F32_EPS * (np.abs(y_ref) + bound2))["max_err_over_bound"] <= 1.0
+    z2 = o.preactivation64(layer2)
+    zero = (z2 <= 0) & (np.abs(z2) > bound2)
+    assert zero.sum() > 1000
+    assert o.bitwise_diff(y_rows[zero], x_rows[zero]) == 0

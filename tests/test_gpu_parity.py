@@ -111,11 +111,19 @@ def test_every_staged_instantiation():
 
 @pytest.mark.parametrize("opts", ["", STAGED.format(128, 128, 8, 8, 32)])
 def test_headline_2048(opts):
-    """The headline shape through the product's check() (reference bound)."""
+    """The headline shape through the product's check() (reference bound), and
+    64 sampled rows of the same output against the oracle: the reference
+    bound and the ReLU-mask gate."""
     d, launch = tg.compile_kernel("mbr", 2048, 2048, 2048, opts or "block-tile=16,16 thread-tile=1,1", tag="test")
     res, out = tg.check("mbr", 2048, 2048, 2048, d, launch)
     assert res["pass"], res
     assert res["err_over_bound"] < 0.05
+    ins = o.make_inputs("mbr", 2048, 2048, 2048)
+    rows = np.sort(np.random.default_rng(3).choice(2048, size=64, replace=False))
+    sub = {"a": ins["a"][rows], "b": ins["b"], "bias": ins["bias"]}
+    ref, bound = o.fp64_reference("mbr", sub)
+    assert o.e1_metrics(out[rows], ref, bound)["max_err_over_bound"] <= 1.0
+    assert o.mask_mismatches(out[rows], o.preactivation64(sub), bound) == 0
 
 
 @pytest.mark.parametrize("workload,shape", [("relu", (999, 1001)), ("bias_add", (33, 17)), ("add", (1024, 1024)),
