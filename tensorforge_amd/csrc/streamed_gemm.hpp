@@ -25,13 +25,16 @@
 //    time share A and B panels in its L2.
 //  * Barriers.  One per slab as in the staged kernel, plus three per tile
 //    around the end-of-tile drain and the Cs writes (see tile_end), so Cs is
-//    never read before it is written or rewritten before it is read.  The bias of a chain that starts with bias_add is loaded into a
-//    register as the tile starts and written to LDS between those barriers,
-//    so the epilogue reads it from LDS.
+//    never read before it is written or rewritten before it is read.  The
+//    bias of a chain that starts with bias_add is loaded into a register as
+//    the tile starts and written to LDS between those barriers, so the
+//    epilogue reads it from LDS.
 //
 // Shapes: M, N, K multiples of BM, BN, BK with K an even number of at least 4
-// slabs (the host pads or refuses); no split-K.  Same arithmetic per output as the staged kernel with the same
-// configuration: the results are bit-identical to it.
+// slabs (the host pads or refuses); no split-K.  C must not overlap an input
+// (the ABI's noalias pointers): a workgroup's first tile receives throwaway
+// stores before its real values.  Same arithmetic per output as the staged
+// kernel with the same configuration: the results are bit-identical to it.
 #pragma once
 
 #include "staged_gemm.hpp"
