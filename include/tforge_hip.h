@@ -42,6 +42,9 @@ extern "C" {
 #define TF_FAMILY_ELEMENTWISE 2 /* programs without a matmul                   */
 #define TF_FAMILY_STREAMED 3    /* tile-k>0 with persistent: one workgroup per CU
                                    streams K slabs over many output tiles      */
+#define TF_FAMILY_WAVEK 4       /* tile-k>0 with wave-split-k: the waves of a
+                                   workgroup split K, partial tiles summed in
+                                   LDS (one launch, no workspace)              */
 
 #define TF_MODE_KERNEL 0 /* the compiled program                            */
 #define TF_MODE_BLAS 1   /* rocBLAS sgemm + a separate epilogue kernel: the
@@ -119,12 +122,14 @@ int tf_device_info(tf_device_info_t *out);
  * launches and select the gfx950 instantiations.  No GPU work: runs on a host
  * without a GPU.  Replaces python/tforge_gpu.py:66-91 (compile_kernel's
  * tool chain).  Options are the reference's (include/TensorForge/Pipelines.h:45-72)
- * plus four backend options: split-k=S (S workgroups per output tile along K,
+ * plus five backend options: split-k=S (S workgroups per output tile along K,
  * then an ordered reduction launch), mask-edges (staged kernels accept shapes
  * that are not tile multiples), persistent (one workgroup per compute unit
  * works through many output tiles, writing each tile's C during the next
- * tile's matrix work; bit-identical to the same configuration without it) and
- * xcd-swizzle (default on). */
+ * tile's matrix work; bit-identical to the same configuration without it),
+ * wave-split-k (each wave of a workgroup reduces its own K range of the
+ * workgroup's tile, the partial tiles are added in LDS in wave order: one
+ * launch for shapes with few output tiles) and xcd-swizzle (default on). */
 int tf_compile(const char *source_name, const char *program, const char *options, tf_kernel_t **out);
 void tf_kernel_free(tf_kernel_t *k);
 

@@ -4,7 +4,8 @@ all: model-predicted versus measured time of every configuration of the fused
 mbr (or matmul) kernel, per shape, and the autotuner's record of the best.
 
 Per shape the study builds one `Candidate` per configuration (x split-K
-factor with --split-k) and fills it in three passes:
+factor with --split-k; the wave-split configurations too with --wave-split)
+and fills it in three passes:
 
   compile   tf_compile; a configuration without an instantiation is recorded
             with the compiler's reason and drops out
@@ -77,6 +78,8 @@ class ShapeStudy:
     def __init__(self, args, workload, m, n, k):
         self.args, self.workload, self.shape = args, workload, (m, n, k)
         space = cm.config_space() if args.space == "cdna4" else cm.reference_space()
+        if args.wave_split:
+            space = space + cm.wave_split_space()
         factors = tuple(int(v) for v in args.split_k.split(","))
         suffix = " mask-edges=1" if args.mask_edges else ""
         self.candidates = [Candidate(cfg, cm.options(cfg) + suffix) for cfg in cm.with_splits(space, m, n, k, factors)]
@@ -192,6 +195,8 @@ def cli():
     ap.add_argument("--tuned", default=str(TUNED), help="JSON table the best configuration is recorded in")
     ap.add_argument("--no-record", action="store_true")
     ap.add_argument("--mask-edges", action="store_true", help="every configuration on the true shape, masked edges")
+    ap.add_argument("--wave-split", action="store_true",
+                    help="add the wave-split configurations (wave-split-k=1) to the space")
     ap.add_argument("--prewarm", type=int, default=500, help="untimed launches before the first timing of a shape")
     return ap
 

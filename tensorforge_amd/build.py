@@ -44,15 +44,29 @@ def _units():
     import gen_instances  # noqa: E402
     gen_instances.main()
     units = [CSRC / "runtime.hip", CSRC / "direct_kernels.hip", CSRC / "_gen" / "registry.hip",
-             CSRC / "_gen" / "streamed.hip"]
+             CSRC / "_gen" / "streamed.hip", CSRC / "_gen" / "wavek.hip"]
     units += sorted((CSRC / "_gen").glob("staged_*.hip"))
     return units
+
+
+def _includes(src, seen=None):
+    """src and the project headers it includes, transitively."""
+    seen = set() if seen is None else seen
+    if src in seen or not src.exists():
+        return seen
+    seen.add(src)
+    for name in re.findall(r'^#include\s+"([^"]+)"', src.read_text(), re.M):
+        for base in (src.parent, CSRC, ROOT / "include"):
+            if (base / name).exists():
+                _includes((base / name).resolve(), seen)
+                break
+    return seen
 
 
 def _compile(src, force):
     obj = OUT / (src.parent.name + "_" + src.stem + ".o")
     log = obj.with_suffix(".log")
-    deps = [src] + list(CSRC.glob("*.h")) + list(CSRC.glob("*.hpp")) + [ROOT / "include" / "tforge_hip.h"]
+    deps = sorted(_includes(src.resolve()))
     if not force and obj.exists() and log.exists() and all(obj.stat().st_mtime >= d.stat().st_mtime for d in deps):
         return obj, log.read_text()
     if src.suffix == ".hip":
@@ -85,6 +99,12 @@ def _entry_name(demangled):
     if m:
         bm, bn, tm, tn, bk = m.groups()
         return f"tf_streamed_b{bm}x{bn}_t{tm}x{tn}_k{bk}"
+    m = re.search(r"wavek_gemm_kernel<(\d+), (\d+), (\d+), (\d+)(?:, \d+)?>", demangled)
+    if m:
+        # One kernel serves every thread tile with its thread count.
+        import gen_instances  # noqa: E402  (csrc is on sys.path after _units)
+        bm, bn, nt, bk = (int(x) for x in m.groups())
+        return [gen_instances.wavek_name(bm, bn, tm, tn, bk) for tm, tn in gen_instances.wavek_thread_tiles(bm, bn, nt)]
     m = re.search(r"(direct_gemm|elementwise)_kernel<(\d+), (\d+)>", demangled)
     if m:
         fam = "direct" if m.group(1) == "direct_gemm" else "elementwise"
@@ -108,15 +128,16 @@ def _resources(logs):
     dem = _demangle(list(recs))
     out = {}
     for mangled, rec in recs.items():
-        name = _entry_name(dem[mangled])
-        if name is None:
+        names = _entry_name(dem[mangled])
+        if names is None:
             continue
-        out[name] = {"vgprs": rec.get("VGPRs", -1), "agprs": rec.get("AGPRs", -1), "sgprs": rec.get("TotalSGPRs", -1),
-                     "scratch_bytes": rec.get("ScratchSize [bytes/lane]", 0),
-                     "lds_bytes": rec.get("LDS Size [bytes/block]", 0),
-                     "occupancy_waves_per_simd": rec.get("Occupancy [waves/SIMD]", -1),
-                     "vgpr_spill": rec.get("VGPRs Spill", 0), "sgpr_spill": rec.get("SGPRs Spill", 0),
-                     "symbol": mangled}
+        for name in names if isinstance(names, list) else [names]:
+            out[name] = {"vgprs": rec.get("VGPRs", -1), "agprs": rec.get("AGPRs", -1), "sgprs": rec.get("TotalSGPRs", -1),
+                         "scratch_bytes": rec.get("ScratchSize [bytes/lane]", 0),
+                         "lds_bytes": rec.get("LDS Size [bytes/block]", 0),
+                         "occupancy_waves_per_simd": rec.get("Occupancy [waves/SIMD]", -1),
+                         "vgpr_spill": rec.get("VGPRs Spill", 0), "sgpr_spill": rec.get("SGPRs Spill", 0),
+                         "symbol": mangled}
     return out
 
 

@@ -33,6 +33,16 @@ output tile, each over Kp/S; the tile count is multiplied by S and the K
 steps divided by S, and the reduction launch adds its HBM traffic (S partial
 slices written and read, C written) plus a fixed launch cost.
 
+Wave-split (the wave-split-k backend option, a seventh configuration entry
+1): the waves of a workgroup split its K range and add their partial tiles in
+LDS, each wave loading its own operands (no sharing), so a workgroup pulls
+(BM+BN)*K*4/S bytes from L2 into one CU.  That stream is bounded by the L2
+requests one CU keeps in flight, not by the L2's bandwidth: a loads-only copy
+of the kernel at 64 x 4096 x 4096 moves 1 MiB per CU in ~20 us, about 22 B/clk
+per CU (l2_stream_bytes_per_cycle), against 64 B/clk of fill bandwidth.  The
+model takes the larger of that stream and the MFMA time per CU, plus the LDS
+round trip of the staged A (and B) slabs and the final partial-tile sum.
+
 Constants are AMD's published MI355X figures (256 CUs, 2.4 GHz, FP32 matrix
 256 FLOP/clk/CU, 160 KiB LDS, 8 TB/s HBM); LATENCY and SYNC are assumptions
 calibrated on measurements, and the model only ranks configurations.
@@ -65,6 +75,7 @@ class Target:
     lds_per_cu: int = 160 * 1024
     max_waves_per_simd: int = 8
     launch_s: float = 3e-6              # mfma: one more dependent kernel launch (split-K reduction)
+    l2_stream_bytes_per_cycle: float = 22.0  # mfma: measured per-CU L2 -> register stream (wave-split)
 
 
 # The reference's model (python/costmodel.py:41-46); TF_GPU_SMS / TF_GPU_DRAM_BW as there.
@@ -94,6 +105,13 @@ def _valid_staged(bm, bn, tm, tn, bk):
 def _block(tm, tn):
     """MFMA block edge: 32 when the wave tile (8*TM x 8*TN) is made of 32x32 blocks, else 16."""
     return 32 if (8 * tm) % 32 == 0 and (8 * tn) % 32 == 0 else 16
+
+
+def _wave_lds_bytes(bm, bn, w, bk):
+    # per-wave staging tiles (A, and B for 16-wide blocks) or the W partial tiles, whichever is larger
+    mb = 32 if bm % 32 == 0 and bn % 32 == 0 else 16
+    stage = bm * (bk + (4 if mb == 32 else 8)) + (0 if mb == 32 else bk * (bn + 4))
+    return w * max(stage, bm * (bn + 4)) * 4
 
 
 def _lds_bytes(bm, bn, tm, tn, bk):
@@ -139,37 +157,61 @@ def config_space():
 
 
 def splits_of(cfg):
-    """Split-K factor of a configuration: (BM, BN, TM, TN, BK[, S])."""
+    """Split-K factor of a configuration: (BM, BN, TM, TN, BK[, S[, WAVE]])."""
     return cfg[5] if len(cfg) > 5 else 1
+
+
+def wave_split_of(cfg):
+    """1 for a wave-split configuration (seventh entry), else 0."""
+    return cfg[6] if len(cfg) > 6 else 0
 
 
 def options(cfg):
     bm, bn, tm, tn, bk = cfg[:5]
     s = splits_of(cfg)
     return (f"block-tile={bm},{bn} thread-tile={tm},{tn} tile-k={bk} promote=1 vectorize=1"
-            + (f" split-k={s}" if s > 1 else ""))
+            + (" wave-split-k=1" if wave_split_of(cfg) else "") + (f" split-k={s}" if s > 1 else ""))
 
 
 def name(cfg):
     bm, bn, tm, tn, bk = cfg[:5]
     s = splits_of(cfg)
-    return f"b{bm}x{bn}-t{tm}x{tn}-k{bk}" + (f"-s{s}" if s > 1 else "")
+    return f"b{bm}x{bn}-t{tm}x{tn}-k{bk}" + ("-w" if wave_split_of(cfg) else "") + (f"-s{s}" if s > 1 else "")
 
 
 def kernel_name(cfg):
     bm, bn, tm, tn, bk = cfg[:5]
-    return f"tf_staged_b{bm}x{bn}_t{tm}x{tn}_k{bk}"
+    return f"tf_{'wavek' if wave_split_of(cfg) else 'staged'}_b{bm}x{bn}_t{tm}x{tn}_k{bk}"
+
+
+def _gen_instances():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("tf_gen_instances", PKG / "csrc" / "gen_instances.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def wave_split_space():
+    """Every wave-split instantiation as (BM, BN, TM, TN, BK, 1, 1): the
+    configurations csrc/gen_instances.py builds."""
+    g = _gen_instances()
+    return [(bm, bn, tm, tn, bk, 1, 1) for bm, bn, nt, bk in g.wavek_configs()
+            for tm, tn in g.wavek_thread_tiles(bm, bn, nt)]
 
 
 def with_splits(space, m, n, k, splits=(1, 2, 4, 8, 16)):
     """Each configuration once per split-K factor that leaves every split at
-    least one K slab (S = 1 keeps the 5-entry form)."""
+    least one K slab (S = 1 keeps the 5-entry form of a staged configuration)."""
     out = []
     for cfg in space:
         nk = padded(cfg, m, n, k)[2] // cfg[4]
         for s in splits:
             if s <= nk:
-                out.append(tuple(cfg[:5]) if s == 1 else tuple(cfg[:5]) + (s,))
+                if wave_split_of(cfg):
+                    out.append(tuple(cfg[:5]) + (s, 1))
+                else:
+                    out.append(tuple(cfg[:5]) if s == 1 else tuple(cfg[:5]) + (s,))
     return out
 
 
@@ -189,7 +231,7 @@ def estimate_info(cfg, target=MI355X, resources=None):
     occ = rec.get("occupancy_waves_per_simd", target.max_waves_per_simd)
     if occ is None or occ <= 0:
         occ = target.max_waves_per_simd
-    lds = rec.get("lds_bytes", _lds_bytes(bm, bn, tm, tn, bk))
+    lds = rec.get("lds_bytes", _wave_lds_bytes(bm, bn, w, bk) if wave_split_of(cfg) else _lds_bytes(bm, bn, tm, tn, bk))
     by_regs = (occ * target.simds) // w
     by_lds = target.lds_per_cu // lds if lds else by_regs
     return {"blocks_per_sm": max(1, min(by_regs, by_lds, 2048 // threads)), "threads": threads}
@@ -222,6 +264,8 @@ def predict(cfg, padded, info, clock_mhz=None, target=MI355X):
                 "bound": "dram" if t_dram > t_compute else ("smem" if lds_step > fma_step else "fma"),
                 "latency_exposed": exposed > 0, "intensity": 2.0 * bm * bn / (4.0 * (bm + bn))}
     w = threads // 64
+    if wave_split_of(cfg):
+        return _predict_wave_split(cfg, padded, bps, blocks, waves, resident, clock, target)
     mb = _block(tm, tn)
     fm, fn = 8 * tm // mb, 8 * tn // mb
     q = math.ceil(resident * w / target.simds)
@@ -248,6 +292,35 @@ def predict(cfg, padded, info, clock_mhz=None, target=MI355X):
     return {"pred_ms": t * 1e3, "waves": waves, "resident": resident, "blocks": blocks,
             "fma_step": mfma_step, "lds_step": lds_step, "l2_step": l2_step, "bound": bound,
             "latency_exposed": exposed > 0, "waves_per_simd": q,
+            "intensity": 2.0 * bm * bn / (4.0 * (bm + bn))}
+
+
+def _predict_wave_split(cfg, padded, bps, blocks, waves, resident, clock, target):
+    """Wave-split kernel: per round of resident workgroups on a CU, the
+    larger of its MFMA time and its L2 operand stream, plus the staged slabs'
+    LDS round trip, the first slab's latency and the partial-tile sum."""
+    bm, bn, tm, tn, bk = cfg[:5]
+    splits = splits_of(cfg)
+    mp, np_, kp = padded
+    w = (bm // tm) * (bn // tn) // 64
+    kz = kp / splits
+    mfma = resident * 2.0 * bm * bn * kz / (target.simds * 64.0)
+    l2 = resident * (bm + bn) * kz * 4 / target.l2_stream_bytes_per_cycle
+    mb = 32 if bm % 32 == 0 and bn % 32 == 0 else 16
+    staged = bm + (0 if mb == 32 else bn)
+    lds = resident * (2 * staged * kz * 4 + 2 * w * bm * bn * 4) / target.lds_bytes_per_cycle
+    compute = max(mfma, l2, lds)
+    cycles = waves * (compute + target.latency + resident * bm * bn * 4 / target.l2_bytes_per_cycle)
+    t_compute = cycles / (clock * 1e6)
+    t_dram = 4.0 * (mp * kp + kp * np_ + mp * np_ + np_) / target.dram_bw
+    t = max(t_compute, t_dram)
+    if splits > 1:
+        t += (2 * splits + 1) * 4.0 * mp * np_ / target.dram_bw + target.launch_s
+    terms = {"mfma": mfma, "lds": lds, "l2": l2}
+    bound = "dram" if t_dram > t_compute else max(terms, key=terms.get)
+    return {"pred_ms": t * 1e3, "waves": waves, "resident": resident, "blocks": blocks,
+            "fma_step": mfma, "lds_step": lds, "l2_step": l2, "bound": bound,
+            "latency_exposed": False, "waves_per_simd": math.ceil(resident * w / target.simds),
             "intensity": 2.0 * bm * bn / (4.0 * (bm + bn))}
 
 

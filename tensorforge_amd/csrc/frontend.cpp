@@ -578,6 +578,8 @@ bool parse_options(const std::string &text, Options &o, std::string &err) {
       if (!want_bool(o.mask_edges)) return false;
     } else if (key == "persistent") {
       if (!want_bool(o.persistent)) return false;
+    } else if (key == "wave-split-k") {
+      if (!want_bool(o.wave_split_k)) return false;
     } else if (key == "block-tile" || key == "thread-tile") {
       std::vector<int64_t> &dst = key == "block-tile" ? o.block_tile : o.thread_tile;
       if (!parse_list(val, dst)) {

@@ -95,6 +95,64 @@ def streamed_name(c):
     return f"tf_streamed_b{bm}x{bn}_t{tm}x{tn}_k{bk}"
 
 
+# Wave-split instantiations (the wave-split-k option): workgroup tiles with
+# few outputs, whose waves split K.  Keyed by (BM, BN, threads, BK); each
+# thread tile that gives that many threads gets a registry entry.
+WAVEK_TILES = [(16, 16), (16, 32), (32, 16), (32, 32), (16, 64), (64, 16), (32, 64), (64, 32), (64, 64)]
+WAVEK_THREADS = (256, 512, 1024)
+WAVEK_BK = (16, 32, 64)
+
+
+def wavek_valid(bm, bn, nt, bk):
+    """Why a wave-split config cannot be instantiated, or None (mirrors wavek_gemm.hpp)."""
+    w = nt // 64
+    mb = 32 if bm % 32 == 0 and bn % 32 == 0 else 16
+    kc = 256 // mb
+    if bk % kc:
+        return f"tile-k must be a multiple of {kc} for {mb}x{mb} MFMA blocks"
+    fm, fn = bm // mb, bn // mb
+    acc = fm * fn * mb * mb // 64
+    c = bk // kc
+    sb = 0 if mb == 32 else 1  # B staged through LDS for 16-wide MFMA blocks
+    lpr, lprb = bk // 4, bn // 4
+    if 64 % lpr or bm % (64 // lpr):
+        return f"a {bm}x{bk} A slab does not split into whole rows per 128-bit load"
+    if sb and (64 % lprb or bk % (64 // lprb)):
+        return f"a {bk}x{bn} B slab does not split into whole rows per 128-bit load"
+    regs = bm * bk // 64 + (bk * bn // 64 if sb else c * 4 * fn)
+    frag = 2 * (fm * 4 + (fn * 4 if sb else 0))
+    budget = (min(512 // (w // 4), 256) if w >= 4 else 256) - 24
+    if (budget - acc - frag) // regs < 2:
+        return (f"two register sets of a {bk}-deep slab ({regs} VGPRs each), {frag} fragment and {acc} "
+                f"accumulator VGPRs exceed the {budget + 24} VGPRs per wave at {w} waves")
+    stage = bm * (bk + (4 if mb == 32 else 8)) + (bk * (bn + (8 if mb == 32 else 4)) if sb else 0)
+    lds = w * max(stage, bm * (bn + 4)) * 4
+    if lds > LDS_LIMIT:
+        return f"{w} staging / partial tiles of {bm}x{bn} ({lds} B) exceed 160 KiB of LDS"
+    return None
+
+
+def wavek_configs():
+    out = []
+    for bm, bn in WAVEK_TILES:
+        for nt in WAVEK_THREADS:
+            for bk in WAVEK_BK:
+                if wavek_valid(bm, bn, nt, bk) is None:
+                    out.append((bm, bn, nt, bk))
+    return out
+
+
+def wavek_thread_tiles(bm, bn, nt):
+    """(TM, TN) pairs with (BM/TM)*(BN/TN) = nt."""
+    per = bm * bn // nt
+    return [(tm, tn) for tm in (1, 2, 4, 8) for tn in (1, 2, 4, 8)
+            if tm * tn == per and bm % tm == 0 and bn % tn == 0]
+
+
+def wavek_name(bm, bn, tm, tn, bk):
+    return f"tf_wavek_b{bm}x{bn}_t{tm}x{tn}_k{bk}"
+
+
 def staging_vectors(bm, bn, tm, tn, bk, vec=1):
     """Global-load vectors (128-bit, or 32-bit without vectorize) a thread stages per slab."""
     threads = (bm // tm) * (bn // tn)
@@ -149,9 +207,30 @@ def main(shards=16):
     p = gen / "streamed.hip"
     if not p.exists() or p.read_text() != text:
         p.write_text(text)
+    lines = ['#include "../wavek_gemm.hpp"', "", "namespace tfk {", "",
+             "#ifndef __HIP_DEVICE_COMPILE__  // host registry data", "extern const KernelEntry kWaveK[] = {"]
+    wk = wavek_configs()
+    n_entries = 0
+    for bm, bn, nt, bk in wk:
+        t = f"{bm}, {bn}, {nt}, {bk}"
+        for tm, tn in wavek_thread_tiles(bm, bn, nt):
+            lines.append(f"    KernelEntry{{FAM_WAVEK, {bm}, {bn}, {tm}, {tn}, {bk}, 1, 1, 0, \"{wavek_name(bm, bn, tm, tn, bk)}\",")
+            lines.append(f"                reinterpret_cast<const void *>(&wavek_gemm_kernel<{t}>),")
+            lines.append(f"                &launch_wavek<{t}>, nullptr, WaveKGemm<{t}>::LDS_BYTES}},")
+            n_entries += 1
+    lines += ["};", f"extern const int kWaveKCount = {n_entries};", "#else",
+              "// Device pass: instantiate the kernels the host table names."]
+    for bm, bn, nt, bk in wk:
+        lines.append(f"template __global__ void wavek_gemm_kernel<{bm}, {bn}, {nt}, {bk}>(GemmParams);")
+    lines += ["#endif", "", "}  // namespace tfk", ""]
+    text = "\n".join(lines)
+    p = gen / "wavek.hip"
+    if not p.exists() or p.read_text() != text:
+        p.write_text(text)
     reg = ['#include <vector>', '', '#include "../tf_kernels.h"', '', 'namespace tfk {', '',
            'extern const KernelEntry kDirectEntries[];', 'extern const int kDirectCount;',
-           'extern const KernelEntry kStreamed[];', 'extern const int kStreamedCount;']
+           'extern const KernelEntry kStreamed[];', 'extern const int kStreamedCount;',
+           'extern const KernelEntry kWaveK[];', 'extern const int kWaveKCount;']
     for i in range(shards):
         reg += [f"extern const KernelEntry kStaged{i}[];", f"extern const int kStagedCount{i};"]
     reg += ["", "static const std::vector<KernelEntry> &all_entries() {",
@@ -160,6 +239,7 @@ def main(shards=16):
     for i in range(shards):
         reg.append(f"    r.insert(r.end(), kStaged{i}, kStaged{i} + kStagedCount{i});")
     reg += ["    r.insert(r.end(), kStreamed, kStreamed + kStreamedCount);",
+            "    r.insert(r.end(), kWaveK, kWaveK + kWaveKCount);",
             "    return r;", "  }();", "  return v;", "}", "",
             "const KernelEntry *registry_begin() { return all_entries().data(); }",
             "const KernelEntry *registry_end() { return all_entries().data() + all_entries().size(); }",
@@ -168,7 +248,8 @@ def main(shards=16):
     p = gen / "registry.hip"
     if not p.exists() or p.read_text() != text:
         p.write_text(text)
-    print(f"{len(cfgs)} staged instantiations in {shards} shards, {len(STREAMED)} streamed")
+    print(f"{len(cfgs)} staged instantiations in {shards} shards, {len(STREAMED)} streamed, "
+          f"{len(wk)} wave-split ({n_entries} entries)")
 
 
 if __name__ == "__main__":

@@ -144,8 +144,27 @@ int select_launches(tf_kernel *k) {
       else if (o.bm * st.K >= (1L << 31) || o.tile_k * st.N >= (1L << 31)) why = "persistent supports BM*K and BK*N below 2^31";
       if (!why.empty()) return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc, "tforge-gpu-pipeline: " + why));
     }
+    // wave-split-k: the wave-split kernel for GEMM stages.
+    const bool wavek = o.wave_split_k && gemm;
+    if (wavek) {
+      std::string why;
+      if (!staged) why = "wave-split-k needs tile-k";
+      else if (masked) why = "wave-split-k needs M, N and K to be multiples of the block and K tiles (pad the problem)";
+      else if (o.persistent) why = "wave-split-k and persistent exclude each other";
+      else if (!o.vectorize) why = "wave-split-k needs vectorize=1";
+      // 32-bit buffer offsets from the tile's origin in A and in B.
+      else if ((o.bm * st.K + st.K) * 4 >= (1L << 31) || (st.K * st.N + o.bn) * 4 >= (1L << 31))
+        why = "wave-split-k supports (BM+1)*K and K*N below 2^29 elements";
+      if (!why.empty()) return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc, "tforge-gpu-pipeline: " + why));
+    }
     for (const tfk::KernelEntry *e = tfk::registry_begin(); e != tfk::registry_end(); ++e) {
-      if (streamed) {
+      if (wavek) {
+        if (e->family == tfk::FAM_WAVEK && e->bm == o.bm && e->bn == o.bn && e->tm == o.tm && e->tn == o.tn &&
+            e->bk == o.tile_k) {
+          L.entry = e;
+          break;
+        }
+      } else if (streamed) {
         if (e->family == tfk::FAM_STREAMED && e->bm == o.bm && e->bn == o.bn && e->tm == o.tm && e->tn == o.tn &&
             e->bk == o.tile_k) {
           L.entry = e;
@@ -177,6 +196,11 @@ int select_launches(tf_kernel *k) {
                                                       " vectors per slab (at most 16); use more threads or a smaller "
                                                       "tile-k, or pad the problem"));
     }
+    if (!L.entry && wavek)
+      return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc,
+                                                "tforge-gpu-pipeline: wave-split-k has no instantiation of this "
+                                                "configuration; wave-split configurations are listed by "
+                                                "tf_registry_entry"));
     if (!L.entry && streamed)
       return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc,
                                                 "tforge-gpu-pipeline: persistent has no instantiation of this "
@@ -236,7 +260,7 @@ int launch_stage(const tf_kernel *k, size_t s, void *const *ptrs, void *ws, hipS
   if (st.M == 0 || st.N == 0) return TF_OK;
   // 128-bit accesses need 16-byte aligned buffers (the reference's ABI
   // guarantees 256-byte alignment: docs/stage8.md:34).
-  if (L.entry->family == tfk::FAM_STAGED || L.entry->family == tfk::FAM_STREAMED) {
+  if (L.entry->family == tfk::FAM_STAGED || L.entry->family == tfk::FAM_STREAMED || L.entry->family == tfk::FAM_WAVEK) {
     std::vector<int> ids = {st.a, st.b, st.out};
     for (const tff::EpiOp &e : st.epi)
       if (e.buf >= 0) ids.push_back(e.buf);

@@ -246,10 +246,7 @@ staged_gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int it = 0; it < G::B_PER; ++it) {
           const int q = tid + it * NT;
-          if (G::B_VECS % NT == 0 || q < G::B_VECS) {
-            const int r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
-            rb[set][it] = *reinterpret_cast<const VT *>(b_src[it] + k0 * ldb);
-          }
+          if (G::B_VECS % NT == 0 || q < G::B_VECS) rb[set][it] = *reinterpret_cast<const VT *>(b_src[it] + k0 * ldb);
         }
       } else if (!guarded(k0)) {
 #pragma unroll

@@ -5,7 +5,7 @@ TForgeToLinalg.cpp:31-35, 106): the product starts from +0.0, relu is
 maximum(x, +0.0), so a NaN propagates and -0.0 / -inf map to +0.0.  What
 follows from that does not depend on the summation order, so the direct
 FMA kernel, the MFMA kernels (32x32 and 16x16 blocks, bias staged in LDS),
-masked edge tiles and split-K must all give exactly:
+masked edge tiles, split-K and the wave-split kernel must all give exactly:
 
   * a NaN in row r of A makes row r of the output NaN;
   * +inf in row k1 of B makes column c of the product +inf or -inf (the sign
@@ -47,6 +47,9 @@ def _run(workload, m, n, k, options, arrays):
     ((256, 256, 128), STAGED.format(64, 64, 2, 2, 64)),                   # 16x16 blocks
     ((200, 140, 72), STAGED.format(64, 64, 4, 4, 32) + " mask-edges=1"),  # edge tiles, K tail
     ((256, 256, 128), STAGED.format(64, 128, 4, 4, 32) + " split-k=4"),   # partial sums + reduction
+    ((256, 256, 128), STAGED.format(32, 32, 1, 1, 32) + " wave-split-k=1"),  # waves split K, sum in LDS
+    ((256, 256, 128), STAGED.format(16, 64, 1, 1, 16) + " wave-split-k=1"),  # 16x16 blocks, B staged
+    ((256, 256, 128), STAGED.format(32, 32, 2, 1, 16) + " wave-split-k=1 split-k=2"),
 ])
 def test_special_values_through_gemm(workload, shape, options):
     m, n, k = shape

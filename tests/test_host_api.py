@@ -258,6 +258,51 @@ def test_persistent_option_refusals(shape, options, message):
         _lib.Kernel(tc.gen_mlir("mbr", *shape), options)
 
 
+@pytest.mark.parametrize("shape,options,message", [
+    ((1000, 1024, 256), "block-tile=32,32 thread-tile=1,1 tile-k=32 promote=1 vectorize=1 mask-edges=1 "
+     "wave-split-k=1", "wave-split-k needs M, N and K to be multiples"),
+    ((1024, 1024, 256), "block-tile=32,32 thread-tile=1,1 tile-k=32 promote=1 vectorize=1 wave-split-k=1 "
+     "persistent=1", "wave-split-k and persistent exclude each other"),
+    ((1024, 1024, 256), "block-tile=16,16 thread-tile=1,1 wave-split-k=1", "wave-split-k needs tile-k"),
+    ((1024, 1024, 256), "block-tile=32,32 thread-tile=1,1 tile-k=32 promote=1 vectorize=0 wave-split-k=1",
+     "wave-split-k needs vectorize=1"),
+    ((1024, 1024, 256), "block-tile=128,128 thread-tile=8,4 tile-k=32 promote=1 vectorize=1 wave-split-k=1",
+     "wave-split-k has no instantiation of this configuration"),
+    ((64, 65536, 16384), "block-tile=32,32 thread-tile=1,1 tile-k=32 promote=1 vectorize=1 wave-split-k=1",
+     "wave-split-k supports"),
+])
+def test_wave_split_option_refusals(shape, options, message):
+    """The wave-split option's limits are compile-time errors with the reason."""
+    from tensorforge_amd import _lib
+    with pytest.raises(RuntimeError, match=message):
+        _lib.Kernel(tc.gen_mlir("mbr", *shape), options)
+
+
+def test_wave_split_launch_geometry():
+    """The reference's geometry: grid (N/BN, M/BM[, split-k]), block (BN/TN,
+    BM/TM); the block's waves are the K ranges."""
+    from tensorforge_amd import _lib
+    opts = "block-tile=32,32 thread-tile=1,1 tile-k=32 promote=1 vectorize=1 wave-split-k=1"
+    one = _lib.Kernel(tc.gen_mlir("mbr", 64, 4096, 4096), opts).launches()[0]
+    assert one["family"] == "wavek" and one["kernel"] == "tf_wavek_b32x32_t1x1_k32"
+    assert one["grid"] == [128, 2, 1] and one["block"] == [32, 32, 1]
+    two = _lib.Kernel(tc.gen_mlir("mbr", 64, 4096, 4096), opts + " split-k=2").launches()[0]
+    assert two["grid"] == [128, 2, 2]
+
+
+def test_wave_split_configurations_in_the_cost_model():
+    """Every wave-split registry entry is in the cost model's space with the
+    same name, and its options compile to it."""
+    from tensorforge_amd import _lib
+    from tensorforge_amd import costmodel as cm
+    names = {e["name"] for e in _lib.registry() if e["family"] == "wavek"}
+    space = cm.wave_split_space()
+    assert {cm.kernel_name(c) for c in space} == names
+    for cfg in space[::7]:
+        launch = _lib.Kernel(tc.gen_mlir("mbr", 2 * cfg[0], 2 * cfg[1], 4 * cfg[4]), cm.options(cfg)).launches()[0]
+        assert launch["kernel"] == cm.kernel_name(cfg)
+
+
 def test_persistent_launch_geometry():
     """One workgroup per compute unit (256), or one per tile when fewer."""
     from tensorforge_amd import _lib
