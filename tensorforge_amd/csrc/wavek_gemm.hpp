@@ -265,15 +265,6 @@ __global__ void __launch_bounds__(NT) wavek_gemm_kernel(GemmParams p) {
     static_for<NBUF>([&](auto u) __attribute__((always_inline)) {
       constexpr int U = decltype(u)::value;
       load(std::integral_constant<int, (U + NBUF - 1) % NBUF>{}, t + U + NBUF - 1);
-#ifdef WAVEK_PRIO
-      {
-        const int lvl = (t + U) * 4 / (rounds * NBUF);
-        if (lvl == 0) __builtin_amdgcn_s_setprio(3);
-        else if (lvl == 1) __builtin_amdgcn_s_setprio(2);
-        else if (lvl == 2) __builtin_amdgcn_s_setprio(1);
-        else __builtin_amdgcn_s_setprio(0);
-      }
-#endif
       // Keep the requests ahead of this slab's MFMAs: the scheduler would
       // otherwise sink them to their use in the next round.
       __builtin_amdgcn_sched_barrier(0);

@@ -17,6 +17,10 @@ instantiations (the ablation rungs, masked twins included) and from
 promote=1 vectorize=1 ones with xcd-swizzle=0, at random shapes up to 400 and
 split factors up to 3.
 
+A fourth draws 24 wave-split configurations (wave-split-k=1; every entry of
+the cost model's wave-split space is eligible) at random shapes up to 700,
+compiled at the padded shape, with split factors 1, 2 or 3.
+
 Two more families: 32 element-op programs (relu, bias_add, add; shapes up to
 3000 x 8192, half of them with rows of whole workgroup chunks; every thread tile 1..8 x 1..8 that compiles) bit-exact against
 NumPy float32 (python/tforge_gpu.py:116-126), and 16 residual blocks at ragged
@@ -110,8 +114,22 @@ def _variant_draws(count=24, seed=2029):
     return out
 
 
+def _wave_draws(count=24, seed=2030):
+    rng = np.random.default_rng(seed)
+    space = cm.wave_split_space()
+    out = []
+    while len(out) < count:
+        cfg = space[rng.integers(len(space))]
+        m, n, k = (int(v) for v in rng.integers(1, 701, size=3))
+        slabs = cm.padded(cfg, m, n, k)[2] // cfg[4]
+        split = int(rng.choice([1, 1, 2, 3]))
+        out.append((("mbr", "matmul")[rng.integers(2)], (m, n, k), tuple(cfg[:5]), split if split <= slabs else 1))
+    return out
+
+
 DRAWS = _draws()
 VARIANT_DRAWS = _variant_draws()
+WAVE_DRAWS = _wave_draws()
 ELT_DRAWS = _elt_draws()
 RESMLP_DRAWS = _resmlp_draws()
 
@@ -163,6 +181,22 @@ def test_random_variant(workload, shape, cfg, opts, masked):
         if workload == "mbr":
             assert o.mask_mismatches(out, o.preactivation64(ins), bound) == 0
         assert o.bitwise_diff(out, padded) == 0
+
+
+@pytest.mark.parametrize("workload,shape,cfg,split", WAVE_DRAWS,
+                         ids=[f"{d[0]}-{'x'.join(map(str, d[1]))}-b{d[2][0]}x{d[2][1]}-t{d[2][2]}x{d[2][3]}"
+                              f"-k{d[2][4]}-s{d[3]}" for d in WAVE_DRAWS])
+def test_random_wave_split(workload, shape, cfg, split):
+    m, n, k = shape
+    opts = STAGED.format(*cfg) + " wave-split-k=1" + (f" split-k={split}" if split > 1 else "")
+    ins = o.make_inputs(workload, m, n, k)
+    print(f"draw {workload} {shape} {opts}", flush=True)
+    out = _run(workload, m, n, k, opts, ins, logical=cm.padded(cfg, m, n, k))
+    ref, bound = o.fp64_reference(workload, ins)
+    assert not np.isnan(out).any()
+    assert o.e1_metrics(out, ref, bound)["max_err_over_bound"] <= 1.0
+    if workload == "mbr":
+        assert o.mask_mismatches(out, o.preactivation64(ins), bound) == 0
 
 
 @pytest.mark.parametrize("workload,shape,opts", ELT_DRAWS,
