@@ -232,7 +232,10 @@ staged_gemm_kernel(GemmParams p) {
     }
     // `sc` is std::integral_constant<int, set>: the staging set is compile-time
     // even where the lambda is not inlined, so the registers stay registers.
-    auto load_slab = [&](auto sc, int k0) __attribute__((always_inline)) {
+    // `gm` (std::integral_constant<int, 0 or 1>): 0 when the caller knows
+    // the slab is not guarded (the masked kernels' steady state, see the slab
+    // loop), so the guarded branch is not compiled in.
+    auto load_slab = [&](auto sc, auto gm, int k0) __attribute__((always_inline)) {
       constexpr int set = decltype(sc)::value;
       if constexpr (!MASK) {
 #pragma unroll
@@ -248,7 +251,7 @@ staged_gemm_kernel(GemmParams p) {
           const int q = tid + it * NT;
           if (G::B_VECS % NT == 0 || q < G::B_VECS) rb[set][it] = *reinterpret_cast<const VT *>(b_src[it] + k0 * ldb);
         }
-      } else if (!guarded(k0)) {
+      } else if (decltype(gm)::value == 0 || !guarded(k0)) {
 #pragma unroll
         for (int it = 0; it < G::A_PER; ++it) {
           const int q = tid + it * NT;
@@ -287,9 +290,9 @@ staged_gemm_kernel(GemmParams p) {
         }
       }
     };
-    auto store_slab = [&](auto sc, int buf, int k0) __attribute__((always_inline)) {
+    auto store_slab = [&](auto sc, auto gm, int buf, int k0) __attribute__((always_inline)) {
       constexpr int set = decltype(sc)::value;
-      if (MASK && guarded(k0)) {
+      if (MASK && decltype(gm)::value == 1 && guarded(k0)) {
 #pragma unroll
         for (int it = 0; it < G::A_PER; ++it)
 #pragma unroll
@@ -359,26 +362,31 @@ staged_gemm_kernel(GemmParams p) {
     if (bias_early && tid < BN / 4)
       *reinterpret_cast<f32x4 *>(&bias_s[4 * tid]) = *reinterpret_cast<const f32x4 *>(p.epi.ptr[0] + n0 + 4 * tid);
     if (nk > 0) {
-      load_slab(std::integral_constant<int, 0>{}, 0);
-      store_slab(std::integral_constant<int, 0>{}, 0, 0);
-      if (nk > 1) load_slab(std::integral_constant<int, DEPTH - 1>{}, BK);
-      if (DEPTH == 2 && nk > 2) load_slab(std::integral_constant<int, 0>{}, 2 * BK);
+      load_slab(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, 0);
+      store_slab(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, 0, 0);
+      if (nk > 1) load_slab(std::integral_constant<int, DEPTH - 1>{}, std::integral_constant<int, 1>{}, BK);
+      if (DEPTH == 2 && nk > 2) load_slab(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, 2 * BK);
     }
     __syncthreads();
     if (nk > 0) load_frags(0, 0, 0);
     // One slab; P = kt & 1 names its LDS buffer; slab s is staged in set
     // s & 1 (two sets) or 0 (one set), and slab kt + 1 + DEPTH is loaded into
     // the set that slab kt + 1 leaves.
-    auto slab = [&](auto par, int kt) __attribute__((always_inline)) {
+    // `gm` = 0: a masked kernel's steady state, where every slab this one
+    // stores or loads is unguarded and a next slab exists (see the loop
+    // below), so the loads are unconditional and the compiler's waits exact.
+    auto slab = [&](auto par, auto gm, int kt) __attribute__((always_inline)) {
       constexpr int P = decltype(par)::value;
       constexpr int cur = P;
-      const bool more = kt + 1 < nk;
+      constexpr bool steady = decltype(gm)::value == 0;
+      const bool more = steady || kt + 1 < nk;
 #pragma unroll
       for (int kc = 0; kc < C; ++kc) {
         const int fs = kc & 1;
         if (C == 1 && more) {
-          store_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, cur ^ 1, (kt + 1) * BK);
-          if (kt + 1 + DEPTH < nk) load_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, (kt + 1 + DEPTH) * BK);
+          store_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, gm, cur ^ 1, (kt + 1) * BK);
+          if (steady || kt + 1 + DEPTH < nk)
+            load_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, gm, (kt + 1 + DEPTH) * BK);
         }
         if (kc + 1 < C) {
           load_frags(cur, kc + 1, fs ^ 1);
@@ -425,8 +433,9 @@ staged_gemm_kernel(GemmParams p) {
         __builtin_amdgcn_sched_barrier(0);
         if (C >= 2 && kc == MID && more) {
           __builtin_amdgcn_sched_barrier(0);
-          store_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, cur ^ 1, (kt + 1) * BK);
-          if (kt + 1 + DEPTH < nk) load_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, (kt + 1 + DEPTH) * BK);
+          store_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, gm, cur ^ 1, (kt + 1) * BK);
+          if (steady || kt + 1 + DEPTH < nk)
+            load_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, gm, (kt + 1 + DEPTH) * BK);
         }
       }
       // With an odd chunk count the next slab's first fragments landed in
@@ -440,12 +449,29 @@ staged_gemm_kernel(GemmParams p) {
           for (int s = 0; s < 4; ++s) bf[0][j][s] = bf[1][j][s];
       }
     };
+    using Steady = std::integral_constant<int, 0>;
+    using Any = std::integral_constant<int, 1>;
     int kt = 0;
-    for (; kt + 1 < nk; kt += 2) {
-      slab(std::integral_constant<int, 0>{}, kt);
-      slab(std::integral_constant<int, 1>{}, kt + 1);
+    // (Not for the configurations whose accumulators fill the register file,
+    // 32768 per workgroup: the second copy of the loop would spill.)
+    if constexpr (MASK && NT * TM * TN < 32768) {
+      // Masked kernels: only the slab holding row K-1 (the last) is guarded
+      // (every slab when N < 4).  While slab kt's loads (slab kt + 1 + DEPTH)
+      // stay before it, run a loop without the guarded branch: a branch
+      // between element-wise and vector loads leaves the compiler unsure how
+      // many loads are in flight, and it then waits for all of them
+      // (vmcnt(0)) three times per slab pair.
+      const int steady = Ni < 4 ? 0 : max(0, nk - 2 - DEPTH) & ~1;
+      for (; kt < steady; kt += 2) {
+        slab(std::integral_constant<int, 0>{}, Steady{}, kt);
+        slab(std::integral_constant<int, 1>{}, Steady{}, kt + 1);
+      }
     }
-    if (kt < nk) slab(std::integral_constant<int, 0>{}, kt);
+    for (; kt + 1 < nk; kt += 2) {
+      slab(std::integral_constant<int, 0>{}, Any{}, kt);
+      slab(std::integral_constant<int, 1>{}, Any{}, kt + 1);
+    }
+    if (kt < nk) slab(std::integral_constant<int, 0>{}, Any{}, kt);
   } else {
     // promote=0: fragments straight from global memory, no LDS, no barriers.
     const float *ag = A + (long)(wm * WTM + lr) * lda + 4 * lg;
