@@ -30,9 +30,13 @@ RESOURCES = PKG / "kernel_resources.json"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
-# Packed FP32 (v_pk_*_f32) is disabled for all device code.
+# Packed FP32 (v_pk_*_f32) is disabled for all device code.  Kernel-argument
+# preloading: a kernel's leading scalar arguments (up to 16 SGPRs) arrive in
+# SGPRs at wave launch instead of through loads from the argument segment
+# (the staged GEMM kernels lead with the fields their prologue needs).
 HIP_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC", "-Wall",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             "-mllvm", "-amdgpu-kernarg-preload-count=16",
              "-I", str(ROOT / "include"), "-I", str(CSRC),
              "-Rpass-analysis=kernel-resource-usage"]
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-I", str(ROOT / "include"), "-I", str(CSRC),

@@ -184,7 +184,8 @@ def main(shards=16):
                   "// Device pass: instantiate the kernels the host table names."]
         for c in part:
             t = ", ".join(str(x) for x in c)
-            lines.append(f"template __global__ void staged_gemm_kernel<{t}>(GemmParams);")
+            lines.append(f"template __global__ void staged_gemm_kernel<{t}>(const float *, const float *, long, long, int, "
+                         "int, int, int, int, int, GemmParams);")
         lines += ["#endif", "", "}  // namespace tfk", ""]
         text = "\n".join(lines)
         p = gen / f"staged_{i:02d}.hip"

@@ -135,9 +135,26 @@ struct StagedGemm {
   static_assert(LDS_BYTES <= 160 * 1024, "LDS per workgroup exceeds 160 KB");
 };
 
+// The kernel's first ten arguments repeat the fields of `p` that the prologue
+// needs before its first global loads, as scalars: the library is built with
+// kernel-argument preloading (-mllvm -amdgpu-kernarg-preload-count), so the
+// hardware puts scalar leading arguments in SGPRs at wave launch, while the
+// by-value struct is read from the kernel-argument segment (a ~1.5k-cycle
+// round trip measured at the start of every wave).  gx, gy = gridDim.x, .y;
+// flags = swizzle | splits << 8.
 template <int BM, int BN, int TM, int TN, int BK, int PROMOTE, int VEC, int MASK>
 __global__ void __launch_bounds__((BM / TM) * (BN / TN))
-staged_gemm_kernel(GemmParams p) {
+staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int pK, int gx, int gy, int flags, int pM,
+                   int pN, GemmParams p) {
+  p.A = pA;
+  p.B = pB;
+  p.lda = plda;
+  p.ldb = pldb;
+  p.K = pK;
+  p.M = pM;
+  p.N = pN;
+  p.swizzle = flags & 255;
+  p.splits = flags >> 8;
   using G = StagedGemm<BM, BN, TM, TN, BK, PROMOTE, VEC>;
   constexpr int NT = G::NT, WTM = G::WTM, WTN = G::WTN, NWN = G::NWN, FM = G::FM, FN = G::FN;
   constexpr int LDA = G::LDA, LDB = G::LDB, VW = G::VW, MB = G::MB, KC = G::KC;
@@ -149,14 +166,15 @@ staged_gemm_kernel(GemmParams p) {
   const int lr = lane % MB, lg = lane / MB;  // row/column within a block, k group
 
   int tile_m, tile_n;
-  staged_tile_coords(gridDim.x, gridDim.y, p.swizzle, tile_m, tile_n);
+  staged_tile_coords(gx, gy, p.swizzle, tile_m, tile_n);
   const long m0 = (long)tile_m * BM, n0 = (long)tile_n * BN;
   const long lda = p.lda, ldb = p.ldb;
   // Split-K: workgroup z reduces K slabs [kb, ke).
   const int nk_all = (p.K + BK - 1) / BK;
   const int splits = p.splits > 1 ? p.splits : 1, split = blockIdx.z;
-  const int kb = (int)((long)nk_all * split / splits);
-  const int ke = (int)((long)nk_all * (split + 1) / splits);
+  // (No 64-bit division in the common single-split case.)
+  const int kb = splits == 1 ? 0 : (int)((long)nk_all * split / splits);
+  const int ke = splits == 1 ? nk_all : (int)((long)nk_all * (split + 1) / splits);
   const long kbase = (long)kb * BK;
   const float *__restrict__ A = p.A + m0 * lda + kbase;
   const float *__restrict__ B = p.B + n0 + kbase * ldb;
@@ -359,10 +377,12 @@ staged_gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) bf[slot][j][s] = bs[s * LDB + j * MB];
     };
+    // Slab 0's loads go out first: the bias test reads the epilogue fields
+    // from the kernel-argument segment, and its wait would delay them.
+    if (nk > 0) load_slab(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, 0);
     if (bias_early && tid < BN / 4)
       *reinterpret_cast<f32x4 *>(&bias_s[4 * tid]) = *reinterpret_cast<const f32x4 *>(p.epi.ptr[0] + n0 + 4 * tid);
     if (nk > 0) {
-      load_slab(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, 0);
       store_slab(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, 0, 0);
       if (nk > 1) load_slab(std::integral_constant<int, DEPTH - 1>{}, std::integral_constant<int, 1>{}, BK);
       if (DEPTH == 2 && nk > 2) load_slab(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, 2 * BK);
@@ -593,7 +613,8 @@ staged_gemm_kernel(GemmParams p) {
 
 template <int BM, int BN, int TM, int TN, int BK, int PROMOTE, int VEC, int MASK>
 hipError_t launch_staged(const GemmParams &p, dim3 grid, dim3 block, hipStream_t stream) {
-  hipLaunchKernelGGL((staged_gemm_kernel<BM, BN, TM, TN, BK, PROMOTE, VEC, MASK>), grid, block, 0, stream, p);
+  hipLaunchKernelGGL((staged_gemm_kernel<BM, BN, TM, TN, BK, PROMOTE, VEC, MASK>), grid, block, 0, stream, p.A, p.B,
+                     p.lda, p.ldb, p.K, (int)grid.x, (int)grid.y, p.swizzle | (p.splits << 8), p.M, p.N, p);
   return hipGetLastError();
 }
 
