@@ -222,7 +222,8 @@ def main(shards=16):
     lines += ["};", f"extern const int kWaveKCount = {n_entries};", "#else",
               "// Device pass: instantiate the kernels the host table names."]
     for bm, bn, nt, bk in wk:
-        lines.append(f"template __global__ void wavek_gemm_kernel<{bm}, {bn}, {nt}, {bk}>(GemmParams);")
+        lines.append(f"template __global__ void wavek_gemm_kernel<{bm}, {bn}, {nt}, {bk}>(const float *, const float *, long, "
+                     "long, int, int, int, int, GemmParams);")
     lines += ["#endif", "", "}  // namespace tfk", ""]
     text = "\n".join(lines)
     p = gen / "wavek.hip"

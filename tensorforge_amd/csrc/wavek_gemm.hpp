@@ -123,8 +123,20 @@ struct WaveKGemm {
   static_assert(LDS_BYTES <= 160 * 1024, "partial tiles exceed 160 KB of LDS");
 };
 
+// The first eight arguments repeat the fields of `p` the prologue needs, as
+// scalars the hardware preloads into SGPRs (as for the staged kernels: the
+// library is built with kernel-argument preloading); gx, gy = gridDim.x, .y;
+// flags = swizzle | splits << 8.
 template <int BM, int BN, int NT, int BK, int SB = wavek_stage_b<BM, BN>()>
-__global__ void __launch_bounds__(NT) wavek_gemm_kernel(GemmParams p) {
+__global__ void __launch_bounds__(NT) wavek_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int pK,
+                                                        int gx, int gy, int flags, GemmParams p) {
+  p.A = pA;
+  p.B = pB;
+  p.lda = plda;
+  p.ldb = pldb;
+  p.K = pK;
+  p.swizzle = flags & 255;
+  p.splits = flags >> 8;
   using G = WaveKGemm<BM, BN, NT, BK, SB>;
   constexpr int W = G::W, MB = G::MB, KC = G::KC, C = G::C, FM = G::FM, FN = G::FN, NBUF = G::NBUF;
   constexpr int LDP = G::LDP, LDA = G::LDA, LPR = G::LPR, RPI = G::RPI, A_INSTR = G::A_INSTR;
@@ -139,7 +151,7 @@ __global__ void __launch_bounds__(NT) wavek_gemm_kernel(GemmParams p) {
   const int lr = lane % MB, lg = lane / MB;
 
   int tile_m, tile_n;
-  staged_tile_coords(gridDim.x, gridDim.y, p.swizzle, tile_m, tile_n);
+  staged_tile_coords(gx, gy, p.swizzle, tile_m, tile_n);
   const long m0 = (long)tile_m * BM, n0 = (long)tile_n * BN;
   const int lda = (int)p.lda, ldb = (int)p.ldb;
 
@@ -148,7 +160,8 @@ __global__ void __launch_bounds__(NT) wavek_gemm_kernel(GemmParams p) {
   // [nk*z/S, nk*(z+1)/S); its waves split that range.
   const int nk_all = p.K / BK;
   const int splits = p.splits > 1 ? p.splits : 1, split = blockIdx.z;
-  const int zb = (int)((long)nk_all * split / splits), nkz = (int)((long)nk_all * (split + 1) / splits) - zb;
+  const int zb = splits == 1 ? 0 : (int)((long)nk_all * split / splits);
+  const int nkz = splits == 1 ? nk_all : (int)((long)nk_all * (split + 1) / splits) - zb;
   const int kb = zb + nkz * wave / W, ke = zb + nkz * (wave + 1) / W, nk = ke - kb;
 
   // Buffer resources over the tile's A panel and B columns; zero records for
@@ -312,7 +325,8 @@ __global__ void __launch_bounds__(NT) wavek_gemm_kernel(GemmParams p) {
 
 template <int BM, int BN, int NT, int BK, int SB = wavek_stage_b<BM, BN>()>
 hipError_t launch_wavek(const GemmParams &p, dim3 grid, dim3 block, hipStream_t stream) {
-  hipLaunchKernelGGL((wavek_gemm_kernel<BM, BN, NT, BK, SB>), grid, block, 0, stream, p);
+  hipLaunchKernelGGL((wavek_gemm_kernel<BM, BN, NT, BK, SB>), grid, block, 0, stream, p.A, p.B, p.lda, p.ldb, p.K,
+                     (int)grid.x, (int)grid.y, p.swizzle | (p.splits << 8), p);
   return hipGetLastError();
 }
 
