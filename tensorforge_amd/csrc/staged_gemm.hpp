@@ -563,8 +563,10 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
 
   if (MASK && (edge || (p.ldc & 3) != 0)) {
     // Edge tile, or rows of C not 16-byte aligned: outputs outside C are
-    // dropped.  With N % 4 == 0 each group of 4 is wholly inside or outside.
-    const bool c_vec = (p.ldc & 3) == 0;
+    // dropped.  A group of 4 wholly inside C is written with one 128-bit
+    // store at 4-byte alignment (16-byte aligned when N % 4 == 0, where every
+    // group is wholly inside or outside); only a group that crosses column N
+    // is written element by element.
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const long m = row_of(i);
@@ -575,8 +577,8 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
         for (int g = 0; g < NG; ++g) {
           const int n = col_of(j, g);
           if (n >= p.N) continue;
-          if (c_vec) {
-            *reinterpret_cast<f32x4 *>(p.C + m * p.ldc + n) = apply_epi4(group(i, j, g), p.epi, m, n);
+          if (n + 4 <= p.N) {
+            *reinterpret_cast<f32x4_u *>(p.C + m * p.ldc + n) = apply_epi4_rows(group(i, j, g), p.epi, m, n);
           } else {
             const f32x4 v = apply_epi4_edge(group(i, j, g), p.epi, m, n, p.N);
             for (int e = 0; e < 4 && n + e < p.N; ++e) p.C[m * p.ldc + n + e] = v[e];
