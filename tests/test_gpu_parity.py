@@ -429,6 +429,26 @@ def test_masked_resmlp_ragged():
     assert tg._resmlp_check(ins, y)["pass"]
 
 
+@pytest.mark.parametrize("shape", [(77, 45, 53), (130, 258, 97), (9, 6, 3)])
+@pytest.mark.parametrize("cfg", [(64, 64, 4, 4, 32), (64, 64, 2, 2, 64)])
+def test_masked_resmlp_unaligned_rows_equal_unfused_bits(shape, cfg):
+    """Residual block with mask-edges at shapes whose rows are not 16-byte
+    aligned (n, k not multiples of 4): the fused epilogue (bias, relu, add of
+    the row-indexed residual) writes the bits of the unfused program, where
+    each element op is its own launch on the same GEMM output."""
+    m, n, k = shape
+    ins = tc.make_inputs("resmlp", m, n, k)
+    arrays = [np.ascontiguousarray(v) for v in ins.values()]
+    outs = []
+    for extra in ("", " fuse-elementwise=0"):
+        kern = _lib.Kernel(tc.gen_mlir("resmlp", m, n, k), STAGED.format(*cfg) + " mask-edges=1" + extra, "t.mlir")
+        y = np.empty((m, n), np.float32)
+        kern.run(arrays, y)
+        outs.append(y)
+    assert o.bitwise_diff(outs[0], outs[1]) == 0
+    assert tg._resmlp_check(ins, outs[0])["pass"]
+
+
 def test_info_and_bench_keys():
     d, launch = tg.compile_kernel("mbr", 1024, 1024, 1024, STAGED.format(128, 128, 8, 8, 32), tag="test")
     inf = tg.info("mbr", 1024, 1024, 1024, d, launch)
