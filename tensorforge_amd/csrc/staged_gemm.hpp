@@ -99,6 +99,15 @@ __device__ __forceinline__ void staged_tile_coords(int gx, int gy, int swizzle, 
   tile_coords(blockIdx.y * gx + blockIdx.x, gx, gy, swizzle, tm, tn);
 }
 
+// Calls f(integral_constant<0>), ..., f(integral_constant<N-1>) in order.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (N > 0) {
+    static_for<N - 1>(f);
+    f(std::integral_constant<int, N - 1>{});
+  }
+}
+
 // Write element e of a staging register (a float or a 4-vector).
 __device__ __forceinline__ void put(float &v, int, float x) { v = x; }
 __device__ __forceinline__ void put(f32x4 &v, int e, float x) { v[e] = x; }
@@ -355,8 +364,53 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
     // MID < C - 1 whenever C >= 2, so slab t+1's stores always precede the
     // barrier at chunk C-1; with a single chunk they are issued before it.
     constexpr int C = BK / KC, MID = C >= 2 ? C / 2 - 1 : 0;
+    // Staging spread over the MFMAs (steady-state slabs of unmasked kernels
+    // with one wave per SIMD): after each of the first 2 * NSTG MFMAs of the
+    // chunks before the barrier, one staging operation -- the LDS write of
+    // vector i, then the global load that refills its registers -- so the
+    // wave always has an MFMA to issue.  With one wave per SIMD nothing
+    // else covers a burst of writes and loads (measured: 64x64 t4x4 k32 at
+    // 1024^3 20.8 -> 19.3 us, 128x128 t8x8 k32 at 2048^3 138.8 -> 126.9 us);
+    // with two or more waves per SIMD the burst is covered and the spread
+    // form is no faster.
+    constexpr int NSTG = G::A_PER + G::B_PER, NMC = 4 * FM * FN;
+    // (Only with the two staging sets of a thread that stages at most 8
+    // vectors: the one-wave 64x64 t8x8 k64 stages 32, and its second copy of
+    // the loop would spill.)
+    constexpr bool SPREAD = !MASK && NT <= 256 && DEPTH == 2 && C >= 2 && 2 * NSTG <= NMC * (C - 1);
     f32x4 af[2][FM];
     float bf[2][FN][4];
+    // One staging vector (item q < A_PER: A, else B) of an unmasked kernel.
+    auto load_item = [&](auto sc, auto qc, int k0) __attribute__((always_inline)) {
+      constexpr int set = decltype(sc)::value, it = decltype(qc)::value;
+      if constexpr (it < G::A_PER) {
+        const int q = tid + it * NT;
+        if (G::A_VECS % NT == 0 || q < G::A_VECS) {
+          const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
+          ra[set][it] = *reinterpret_cast<const VT *>(A + r * lda + k0 + c);
+        }
+      } else {
+        const int q = tid + (it - G::A_PER) * NT;
+        if (G::B_VECS % NT == 0 || q < G::B_VECS)
+          rb[set][it - G::A_PER] = *reinterpret_cast<const VT *>(b_src[it - G::A_PER] + k0 * ldb);
+      }
+    };
+    auto store_item = [&](auto sc, auto qc, int buf) __attribute__((always_inline)) {
+      constexpr int set = decltype(sc)::value, it = decltype(qc)::value;
+      if constexpr (it < G::A_PER) {
+        const int q = tid + it * NT;
+        if (G::A_VECS % NT == 0 || q < G::A_VECS) {
+          const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
+          *reinterpret_cast<VT *>(&As[buf][r * LDA + c]) = ra[set][it];
+        }
+      } else {
+        const int q = tid + (it - G::A_PER) * NT;
+        if (G::B_VECS % NT == 0 || q < G::B_VECS) {
+          const int r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
+          *reinterpret_cast<VT *>(&Bs[buf][r * LDB + c]) = rb[set][it - G::A_PER];
+        }
+      }
+    };
     auto load_frags = [&](int buf, int kc, int slot) __attribute__((always_inline)) {
       const float *as = As[buf] + (wm * WTM + lr) * LDA + 4 * lg + kc * KC;
       const float *bs = Bs[buf] + (4 * lg + kc * KC) * LDB + wn * WTN + lr;
@@ -414,13 +468,38 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
           __syncthreads();
           load_frags(cur ^ 1, 0, fs ^ 1);
         }
+        constexpr bool spread = SPREAD && steady;
+        if constexpr (spread) {
+          constexpr int SET = DEPTH == 2 ? (P ^ 1) : 0;
+          static_for<NMC>([&](auto xc) __attribute__((always_inline)) {
+            constexpr int x = decltype(xc)::value;
+            constexpr int s = x / (FM * FN), i = (x / FN) % FM, j = x % FN;
+            acc[i][j] = mfma_block<MB>(bf[fs][j][s], af[fs][i][s], acc[i][j]);
+            const int op = kc * NMC + x;  // constant once the chunk loop is unrolled
+            if (kc < C - 1 && op < 2 * NSTG) {
+              __builtin_amdgcn_sched_barrier(0);
+              static_for<2 * NSTG>([&](auto oc) __attribute__((always_inline)) {
+                constexpr int o = decltype(oc)::value;
+                if (o == op) {
+                  if constexpr (o % 2 == 0)
+                    store_item(std::integral_constant<int, SET>{}, std::integral_constant<int, o / 2>{}, cur ^ 1);
+                  else
+                    load_item(std::integral_constant<int, SET>{}, std::integral_constant<int, o / 2>{},
+                              (kt + 1 + DEPTH) * BK);
+                }
+              });
+              __builtin_amdgcn_sched_barrier(0);
+            }
+          });
+        } else {
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+          for (int s = 0; s < 4; ++s)
 #pragma unroll
-          for (int i = 0; i < FM; ++i)
+            for (int i = 0; i < FM; ++i)
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
-              acc[i][j] = mfma_block<MB>(bf[fs][j][s], af[fs][i][s], acc[i][j]);
+              for (int j = 0; j < FN; ++j)
+                acc[i][j] = mfma_block<MB>(bf[fs][j][s], af[fs][i][s], acc[i][j]);
+        }
         // Order of this chunk's MFMAs and the next chunk's fragment reads,
         // chosen by measurement on MI355X (main-loop shader cycles at 2048^3,
         // launch times at 1024^3 and 4096^3 over 10 configurations):
@@ -429,7 +508,9 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
         //   several blocks, <= 8 waves: all reads 2 MFMAs before the end;
         //   several blocks, 16 waves:  MFMA, read, repeated.
         constexpr int NM = 4 * FM * FN;  // MFMAs per chunk
-        if constexpr (FM * FN == 1 && MB == 32) {
+        if constexpr (spread) {
+          // (order fixed above)
+        } else if constexpr (FM * FN == 1 && MB == 32) {
           __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
           __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS read
           __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
@@ -451,7 +532,7 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
           }
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (C >= 2 && kc == MID && more) {
+        if (!spread && C >= 2 && kc == MID && more) {
           __builtin_amdgcn_sched_barrier(0);
           store_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, gm, cur ^ 1, (kt + 1) * BK);
           if (steady || kt + 1 + DEPTH < nk)
@@ -474,14 +555,16 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
     int kt = 0;
     // (Not for the configurations whose accumulators fill the register file,
     // 32768 per workgroup: the second copy of the loop would spill.)
-    if constexpr (MASK && NT * TM * TN < 32768) {
+    if constexpr ((MASK || SPREAD) && NT * TM * TN < 32768) {
       // Masked kernels: only the slab holding row K-1 (the last) is guarded
       // (every slab when N < 4).  While slab kt's loads (slab kt + 1 + DEPTH)
       // stay before it, run a loop without the guarded branch: a branch
       // between element-wise and vector loads leaves the compiler unsure how
       // many loads are in flight, and it then waits for all of them
-      // (vmcnt(0)) three times per slab pair.
-      const int steady = Ni < 4 ? 0 : max(0, nk - 2 - DEPTH) & ~1;
+      // (vmcnt(0)) three times per slab pair.  Spread kernels: the same
+      // straight-line loop carries the spread staging (its loads are
+      // unconditional there, so each LDS write waits for exactly its load).
+      const int steady = (MASK && Ni < 4) ? 0 : max(0, nk - 2 - DEPTH) & ~1;
       for (; kt < steady; kt += 2) {
         slab(std::integral_constant<int, 0>{}, Steady{}, kt);
         slab(std::integral_constant<int, 1>{}, Steady{}, kt + 1);

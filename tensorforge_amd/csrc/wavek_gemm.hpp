@@ -58,15 +58,6 @@
 
 namespace tfk {
 
-// Calls f(integral_constant<0>), ..., f(integral_constant<N-1>) in order.
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F &&f) {
-  if constexpr (N > 0) {
-    static_for<N - 1>(f);
-    f(std::integral_constant<int, N - 1>{});
-  }
-}
-
 // Buffer resource word 3 for gfx9-family raw buffers (32-bit data format,
 // bounds-checked by byte offset).
 constexpr int kBufferWord3 = 0x00020000;
