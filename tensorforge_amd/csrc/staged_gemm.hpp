@@ -364,8 +364,8 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
     // MID < C - 1 whenever C >= 2, so slab t+1's stores always precede the
     // barrier at chunk C-1; with a single chunk they are issued before it.
     constexpr int C = BK / KC, MID = C >= 2 ? C / 2 - 1 : 0;
-    // Staging spread over the MFMAs (steady-state slabs of unmasked kernels
-    // with one wave per SIMD): after each of the first 2 * NSTG MFMAs of the
+    // Staging spread over the MFMAs (steady-state slabs of kernels with one
+    // wave per SIMD): after each of the first 2 * NSTG MFMAs of the
     // chunks before the barrier, one staging operation -- the LDS write of
     // vector i, then the global load that refills its registers -- so the
     // wave always has an MFMA to issue.  With one wave per SIMD nothing
@@ -377,22 +377,27 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
     // (Only with the two staging sets of a thread that stages at most 8
     // vectors: the one-wave 64x64 t8x8 k64 stages 32, and its second copy of
     // the loop would spill.)
-    constexpr bool SPREAD = !MASK && NT <= 256 && DEPTH == 2 && C >= 2 && 2 * NSTG <= NMC * (C - 1);
+    constexpr bool SPREAD = PROMOTE && VEC && NT <= 256 && DEPTH == 2 && C >= 2 && 2 * NSTG <= NMC * (C - 1);
     f32x4 af[2][FM];
     float bf[2][FN][4];
-    // One staging vector (item q < A_PER: A, else B) of an unmasked kernel.
+    // One staging vector (item q < A_PER: A, else B) of a slab that is not
+    // guarded (the loads of load_slab's unmasked and unguarded paths).
     auto load_item = [&](auto sc, auto qc, int k0) __attribute__((always_inline)) {
       constexpr int set = decltype(sc)::value, it = decltype(qc)::value;
       if constexpr (it < G::A_PER) {
         const int q = tid + it * NT;
         if (G::A_VECS % NT == 0 || q < G::A_VECS) {
           const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
-          ra[set][it] = *reinterpret_cast<const VT *>(A + r * lda + k0 + c);
+          if constexpr (!MASK) ra[set][it] = *reinterpret_cast<const VT *>(A + r * lda + k0 + c);
+          else ra[set][it] = load16(p.A + (min(m0i + r, Mi - 1) * (int)lda + kbi + k0 + c));
         }
       } else {
-        const int q = tid + (it - G::A_PER) * NT;
-        if (G::B_VECS % NT == 0 || q < G::B_VECS)
-          rb[set][it - G::A_PER] = *reinterpret_cast<const VT *>(b_src[it - G::A_PER] + k0 * ldb);
+        constexpr int ib = it - G::A_PER;
+        const int q = tid + ib * NT;
+        if (G::B_VECS % NT == 0 || q < G::B_VECS) {
+          if constexpr (!MASK) rb[set][ib] = *reinterpret_cast<const VT *>(b_src[ib] + k0 * ldb);
+          else rb[set][ib] = load16(p.B + (b_off[ib] + k0 * (int)ldb));
+        }
       }
     };
     auto store_item = [&](auto sc, auto qc, int buf) __attribute__((always_inline)) {
