@@ -108,6 +108,14 @@ __device__ __forceinline__ void static_for(F &&f) {
   }
 }
 
+// One staging vector (a float or a 4-vector) by a raw buffer load at a byte
+// offset from the resource's base.
+template <typename VT>
+__device__ __forceinline__ VT buffer_load_vt(__amdgpu_buffer_rsrc_t rs, int byte_off) {
+  if constexpr (sizeof(VT) == 16) return __builtin_bit_cast(VT, __builtin_amdgcn_raw_buffer_load_b128(rs, byte_off, 0, 0));
+  else return __builtin_bit_cast(VT, __builtin_amdgcn_raw_buffer_load_b32(rs, byte_off, 0, 0));
+}
+
 // Write element e of a staging register (a float or a 4-vector).
 __device__ __forceinline__ void put(float &v, int, float x) { v = x; }
 __device__ __forceinline__ void put(f32x4 &v, int e, float x) { v[e] = x; }
@@ -262,9 +270,40 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
     // `gm` (std::integral_constant<int, 0 or 1>): 0 when the caller knows
     // the slab is not guarded (the masked kernels' steady state, see the slab
     // loop), so the guarded branch is not compiled in.
-    auto load_slab = [&](auto sc, auto gm, int k0) __attribute__((always_inline)) {
+    // Buffer loads (`bc` = BufOn; unmasked staging): the slab's base
+    // addresses go into two buffer resources (scalar 64-bit arithmetic) and
+    // each thread keeps one 32-bit byte offset per vector, so a global load
+    // carries no 64-bit vector address add.  Between the MFMAs of one wave per
+    // SIMD those adds cost 1.5 us at 1024^3 (64x64 t4x4 k16: 19.3 -> 17.75 us
+    // back to back) and 6 us at 2048^3 (128x128 t8x8 k16: 126.4 -> 120.0 us).
+    // Used only when every offset fits 31 bits (the caller checks BM * lda and
+    // BK * ldb); otherwise the same loop runs with flat loads.
+    using BufOn = std::integral_constant<int, 1>;
+    using BufOff = std::integral_constant<int, 0>;
+    auto buf_rsrc = [](const float *base) __attribute__((always_inline)) {
+      return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), 0, 0x7fffffff, 0x00020000);
+    };
+    auto a_byte = [&](int it) __attribute__((always_inline)) {
+      const int q = tid + it * NT, r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
+      return (int)((r * lda + c) * 4);
+    };
+    auto b_byte = [&](int it) __attribute__((always_inline)) {
+      const int q = tid + it * NT, r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
+      return (int)((r * ldb + c) * 4);
+    };
+    auto load_slab = [&](auto sc, auto gm, int k0, auto bc) __attribute__((always_inline)) {
       constexpr int set = decltype(sc)::value;
-      if constexpr (!MASK) {
+      if constexpr (!MASK && decltype(bc)::value) {
+        const __amdgpu_buffer_rsrc_t rsa = buf_rsrc(A + k0), rsb = buf_rsrc(B + (long)k0 * ldb);
+#pragma unroll
+        for (int it = 0; it < G::A_PER; ++it)
+          if (G::A_VECS % NT == 0 || tid + it * NT < G::A_VECS)
+            ra[set][it] = buffer_load_vt<VT>(rsa, a_byte(it));
+#pragma unroll
+        for (int it = 0; it < G::B_PER; ++it)
+          if (G::B_VECS % NT == 0 || tid + it * NT < G::B_VECS)
+            rb[set][it] = buffer_load_vt<VT>(rsb, b_byte(it));
+      } else if constexpr (!MASK) {
 #pragma unroll
         for (int it = 0; it < G::A_PER; ++it) {
           const int q = tid + it * NT;
@@ -382,9 +421,18 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
     float bf[2][FN][4];
     // One staging vector (item q < A_PER: A, else B) of a slab that is not
     // guarded (the loads of load_slab's unmasked and unguarded paths).
-    auto load_item = [&](auto sc, auto qc, int k0) __attribute__((always_inline)) {
+    auto load_item = [&](auto sc, auto qc, int k0, auto bc) __attribute__((always_inline)) {
       constexpr int set = decltype(sc)::value, it = decltype(qc)::value;
-      if constexpr (it < G::A_PER) {
+      if constexpr (!MASK && decltype(bc)::value) {
+        if constexpr (it < G::A_PER) {
+          if (G::A_VECS % NT == 0 || tid + it * NT < G::A_VECS)
+            ra[set][it] = buffer_load_vt<VT>(buf_rsrc(A + k0), a_byte(it));
+        } else {
+          constexpr int ib = it - G::A_PER;
+          if (G::B_VECS % NT == 0 || tid + ib * NT < G::B_VECS)
+            rb[set][ib] = buffer_load_vt<VT>(buf_rsrc(B + (long)k0 * ldb), b_byte(ib));
+        }
+      } else if constexpr (it < G::A_PER) {
         const int q = tid + it * NT;
         if (G::A_VECS % NT == 0 || q < G::A_VECS) {
           const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
@@ -438,13 +486,14 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
     };
     // Slab 0's loads go out first: the bias test reads the epilogue fields
     // from the kernel-argument segment, and its wait would delay them.
-    if (nk > 0) load_slab(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, 0);
+    if (nk > 0) load_slab(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, 0, BufOff{});
     if (bias_early && tid < BN / 4)
       *reinterpret_cast<f32x4 *>(&bias_s[4 * tid]) = *reinterpret_cast<const f32x4 *>(p.epi.ptr[0] + n0 + 4 * tid);
     if (nk > 0) {
       store_slab(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, 0, 0);
-      if (nk > 1) load_slab(std::integral_constant<int, DEPTH - 1>{}, std::integral_constant<int, 1>{}, BK);
-      if (DEPTH == 2 && nk > 2) load_slab(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, 2 * BK);
+      if (nk > 1) load_slab(std::integral_constant<int, DEPTH - 1>{}, std::integral_constant<int, 1>{}, BK, BufOff{});
+      if (DEPTH == 2 && nk > 2)
+        load_slab(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, 2 * BK, BufOff{});
     }
     __syncthreads();
     if (nk > 0) load_frags(0, 0, 0);
@@ -454,7 +503,7 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
     // `gm` = 0: a masked kernel's steady state, where every slab this one
     // stores or loads is unguarded and a next slab exists (see the loop
     // below), so the loads are unconditional and the compiler's waits exact.
-    auto slab = [&](auto par, auto gm, int kt) __attribute__((always_inline)) {
+    auto slab = [&](auto par, auto gm, int kt, auto bc) __attribute__((always_inline)) {
       constexpr int P = decltype(par)::value;
       constexpr int cur = P;
       constexpr bool steady = decltype(gm)::value == 0;
@@ -465,7 +514,7 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
         if (C == 1 && more) {
           store_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, gm, cur ^ 1, (kt + 1) * BK);
           if (steady || kt + 1 + DEPTH < nk)
-            load_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, gm, (kt + 1 + DEPTH) * BK);
+            load_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, gm, (kt + 1 + DEPTH) * BK, bc);
         }
         if (kc + 1 < C) {
           load_frags(cur, kc + 1, fs ^ 1);
@@ -490,7 +539,7 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
                     store_item(std::integral_constant<int, SET>{}, std::integral_constant<int, o / 2>{}, cur ^ 1);
                   else
                     load_item(std::integral_constant<int, SET>{}, std::integral_constant<int, o / 2>{},
-                              (kt + 1 + DEPTH) * BK);
+                              (kt + 1 + DEPTH) * BK, bc);
                 }
               });
               __builtin_amdgcn_sched_barrier(0);
@@ -541,7 +590,7 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
           __builtin_amdgcn_sched_barrier(0);
           store_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, gm, cur ^ 1, (kt + 1) * BK);
           if (steady || kt + 1 + DEPTH < nk)
-            load_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, gm, (kt + 1 + DEPTH) * BK);
+            load_slab(std::integral_constant<int, DEPTH == 2 ? (P ^ 1) : 0>{}, gm, (kt + 1 + DEPTH) * BK, bc);
         }
       }
       // With an odd chunk count the next slab's first fragments landed in
@@ -557,29 +606,43 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
     };
     using Steady = std::integral_constant<int, 0>;
     using Any = std::integral_constant<int, 1>;
-    int kt = 0;
-    // (Not for the configurations whose accumulators fill the register file,
-    // 32768 per workgroup: the second copy of the loop would spill.)
-    if constexpr ((MASK || SPREAD) && NT * TM * TN < 32768) {
-      // Masked kernels: only the slab holding row K-1 (the last) is guarded
-      // (every slab when N < 4).  While slab kt's loads (slab kt + 1 + DEPTH)
-      // stay before it, run a loop without the guarded branch: a branch
-      // between element-wise and vector loads leaves the compiler unsure how
-      // many loads are in flight, and it then waits for all of them
-      // (vmcnt(0)) three times per slab pair.  Spread kernels: the same
-      // straight-line loop carries the spread staging (its loads are
-      // unconditional there, so each LDS write waits for exactly its load).
-      const int steady = (MASK && Ni < 4) ? 0 : max(0, nk - 2 - DEPTH) & ~1;
-      for (; kt < steady; kt += 2) {
-        slab(std::integral_constant<int, 0>{}, Steady{}, kt);
-        slab(std::integral_constant<int, 1>{}, Steady{}, kt + 1);
+    auto k_loop = [&](auto bc) __attribute__((always_inline)) {
+      int kt = 0;
+      // (Not for the configurations whose accumulators fill the register file,
+      // 32768 per workgroup: the second copy of the loop would spill.)
+      if constexpr ((MASK || SPREAD) && NT * TM * TN < 32768) {
+        // Masked kernels: only the slab holding row K-1 (the last) is guarded
+        // (every slab when N < 4).  While slab kt's loads (slab kt + 1 + DEPTH)
+        // stay before it, run a loop without the guarded branch: a branch
+        // between element-wise and vector loads leaves the compiler unsure how
+        // many loads are in flight, and it then waits for all of them
+        // (vmcnt(0)) three times per slab pair.  Spread kernels: the same
+        // straight-line loop carries the spread staging (its loads are
+        // unconditional there, so each LDS write waits for exactly its load).
+        const int steady = (MASK && Ni < 4) ? 0 : max(0, nk - 2 - DEPTH) & ~1;
+        for (; kt < steady; kt += 2) {
+          slab(std::integral_constant<int, 0>{}, Steady{}, kt, bc);
+          slab(std::integral_constant<int, 1>{}, Steady{}, kt + 1, bc);
+        }
       }
+      for (; kt + 1 < nk; kt += 2) {
+        slab(std::integral_constant<int, 0>{}, Any{}, kt, bc);
+        slab(std::integral_constant<int, 1>{}, Any{}, kt + 1, bc);
+      }
+      if (kt < nk) slab(std::integral_constant<int, 0>{}, Any{}, kt, bc);
+    };
+    // Buffer loads where measured faster: the spread kernels, and the
+    // block-staged ones with tiles of at least 128 x 128 (2048^3 t8x4 k32
+    // 124.9 -> 123.6 us; the 8-wave 64x64 t4x2 k64 at 1024^3 was 2.4% slower
+    // with them).  Not for 1024-thread workgroups (128 VGPRs per lane): the
+    // flat-load copy of the loop beside the buffer one spills there.
+    constexpr bool BUFCAP = !MASK && VEC && NT < 1024 && (SPREAD || BM * BN >= 128 * 128);
+    if constexpr (BUFCAP) {
+      if ((long)BM * lda + BK < (1L << 29) && (long)BK * ldb + BN < (1L << 29)) k_loop(BufOn{});
+      else k_loop(BufOff{});
+    } else {
+      k_loop(BufOff{});
     }
-    for (; kt + 1 < nk; kt += 2) {
-      slab(std::integral_constant<int, 0>{}, Any{}, kt);
-      slab(std::integral_constant<int, 1>{}, Any{}, kt + 1);
-    }
-    if (kt < nk) slab(std::integral_constant<int, 0>{}, Any{}, kt);
   } else {
     // promote=0: fragments straight from global memory, no LDS, no barriers.
     const float *ag = A + (long)(wm * WTM + lr) * lda + 4 * lg;
