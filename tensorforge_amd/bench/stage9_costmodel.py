@@ -14,6 +14,11 @@ and fills it in three passes:
             reference of the shape (err/bound <= 1, exact ReLU masks), then
             tf_bench; with --top N only the N best-predicted are measured
 
+  throughput  (--objective throughput) every timed configuration's rate with
+            launches issued back to back, as bench.py measures its value:
+            one window of 50 launches after 10 untimed ones, then the six
+            best alternate in six rounds and their median windows decide
+
 and then compares: the model's pick (least predicted time, passing) against
 the measured best, raw and clock-adjusted; each one's rank in the other's
 order; and the Spearman rank correlation of predicted and measured times
@@ -21,7 +26,12 @@ order; and the Spearman rank correlation of predicted and measured times
 and the summary columns are the reference's Stage 9 tables
 (bench/stage9_costmodel.py), so both read the same way.  Unless --no-record,
 the best configuration goes into tensorforge_amd/tuned_configs.json, which
-bench.py and costmodel.tuned_options read.
+bench.py and costmodel.tuned_options read: the least per-launch median
+(tf_bench: one event pair per rep, the GPU idle between reps), or with
+--objective throughput the least back-to-back time.  The two orders differ
+where a configuration's ramp at the start and end of a launch, which back to
+back launches overlap, sets it apart: at 2048^3 the 4-wave 64x128 tiles lead
+per launch and the 128x128 thread-tile 8,8 tile back to back.
 
   python -m tensorforge_amd.bench.stage9_costmodel --shapes 2048x2048x2048 \\
       --csv results/gpu/stage9_autotune.csv --summary results/gpu/stage9_summary.csv
@@ -61,6 +71,7 @@ class Candidate:
     info: dict = None        # resources from the occupancy API
     pred: dict = None        # costmodel.predict
     result: "harness.Result" = None
+    window_ms: float = None  # back-to-back ms per launch (throughput objective)
 
     @property
     def name(self):
@@ -124,6 +135,60 @@ class ShapeStudy:
             print(f"  {c.name:>18} {c.measured_ms:.4f} ms {c.result.rate()[1] / 1e3:7.2f} TFLOP/s  "
                   f"pred {c.pred['pred_ms']:.4f} ms", flush=True)
 
+    def throughput(self, warm=10, steps=50, finalists=6, rounds=6):
+        """Back-to-back ms per launch of every timed candidate (one window of
+        `steps` launches after `warm` untimed ones), then of the `finalists`
+        best again over `rounds` alternating rounds (first to last, then last
+        to first), each candidate's median window.  Inputs are uniform [-1, 1]
+        device buffers of the shapes the kernel takes; launches go straight to
+        tf_launch, so the host issues them faster than the shortest kernel
+        here runs."""
+        import statistics
+        import torch
+        from tensorforge_amd import _lib
+        dev = torch.device("cuda:0")
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(1234)
+        stream = torch.cuda.current_stream()
+        pool, bufs, launchers = self.timed(), {}, {}
+
+        def launcher(c):
+            kern = tg._kernel(c.kdir, c.launch)
+            shapes = tuple(tuple(b["shape"]) for b in kern.buffers())
+            if shapes not in bufs:
+                bufs[shapes] = [torch.empty(s, device=dev).uniform_(-1, 1, generator=gen) for s in shapes]
+            arr = (_lib.P * len(shapes))(*[_lib.P(t.data_ptr()) for t in bufs[shapes]])
+            fn, h, st = _lib.lib().tf_launch, kern.h, _lib.P(stream.cuda_stream)
+
+            def window(count):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                bad = sum(fn(h, arr, st) < 0 for _ in range(count))
+                b.record(stream)
+                b.synchronize()
+                if bad:
+                    raise RuntimeError(f"tf_launch failed for {c.name}: {_lib.lib().tf_last_error().decode()}")
+                return a.elapsed_time(b) / count
+            return kern, window
+
+        for c in pool:
+            launchers[c.name] = launcher(c)
+            _, window = launchers[c.name]
+            window(warm)
+            c.window_ms = window(steps)
+        final = sorted(pool, key=lambda c: c.window_ms)[:finalists]
+        times = {c.name: [] for c in final}
+        for r in range(rounds):
+            for c in (final if r % 2 == 0 else final[::-1]):
+                _, window = launchers[c.name]
+                window(warm)
+                times[c.name].append(window(steps))
+        for c in final:
+            c.window_ms = statistics.median(times[c.name])
+            print(f"  {c.name:>18} back to back {c.window_ms * 1e3:.1f} us/launch "
+                  f"(rounds {', '.join(f'{t * 1e3:.1f}' for t in times[c.name])})", flush=True)
+        self.finalists = final
+
     def compiled(self):
         return [c for c in self.candidates if not c.rejected]
 
@@ -134,7 +199,17 @@ class ShapeStudy:
         self._timed("compile", self.compile)
         self._timed("predict", self.predict)
         self._timed("measure", self.measure)
+        if self.args.objective == "throughput" and self.timed():
+            self._timed("throughput", self.throughput)
         return self
+
+    def chosen(self, best):
+        """The configuration the tuned table records: `best` (least per-launch
+        median) or, with the throughput objective, the least back-to-back time
+        among the finalists."""
+        if self.args.objective != "throughput":
+            return best
+        return min(self.finalists, key=lambda c: c.window_ms)
 
     def row_of(self, c):
         p, inf = c.pred, c.info
@@ -144,7 +219,8 @@ class ShapeStudy:
                                     f"occ={inf['theo_occupancy']}"),
                             notes=(f"model: pred_ms={p['pred_ms']:.4f} waves={p['waves']} resident={p['resident']} "
                                    f"bound={p['bound']} fma_step={p['fma_step']:.0f} lds_step={p['lds_step']:.0f} "
-                                   f"latency_exposed={int(p['latency_exposed'])}"))
+                                   f"latency_exposed={int(p['latency_exposed'])}"
+                                   + (f"; back_to_back_ms={c.window_ms:.6f}" if c.window_ms is not None else "")))
 
     def summary(self, base):
         """The summary row (SUMMARY_COLUMNS) and the (pick, best) candidates."""
@@ -169,15 +245,21 @@ class ShapeStudy:
         return row, pick, best, float(rho)
 
 
-def record_best(path, workload, shape, best, pick, rho):
+def record_best(path, workload, shape, best, pick, rho, objective="latency"):
+    """Records `best` for (workload, shape).  "tflops" is at the objective's
+    time: the per-launch median, or the back-to-back time (window_ms)."""
     path = pathlib.Path(path)
     table = json.loads(path.read_text()) if path.exists() else {}
     m, n, k = shape
-    table[f"{workload}/{m}x{n}x{k}"] = {
+    ms = best.window_ms if objective == "throughput" else best.measured_ms
+    entry = {
         "options": best.options, "config": best.name, "median_ms": best.measured_ms,
-        "tflops": 2.0 * m * n * k / (best.measured_ms * 1e-3) / 1e12, "model_pick": pick.name,
+        "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12, "model_pick": pick.name,
         "model_pick_ms": pick.measured_ms, "speedup_over_model_pick": pick.measured_ms / best.measured_ms,
-        "spearman": rho}
+        "spearman": rho, "objective": objective}
+    if objective == "throughput":
+        entry["back_to_back_ms"] = best.window_ms
+    table[f"{workload}/{m}x{n}x{k}"] = entry
     path.write_text(json.dumps(table, indent=1, sort_keys=True) + "\n")
 
 
@@ -198,6 +280,9 @@ def cli():
     ap.add_argument("--wave-split", action="store_true",
                     help="add the wave-split configurations (wave-split-k=1) to the space")
     ap.add_argument("--prewarm", type=int, default=500, help="untimed launches before the first timing of a shape")
+    ap.add_argument("--objective", choices=("latency", "throughput"), default="latency",
+                    help="what the recorded configuration minimises: the per-launch median (tf_bench), or the "
+                         "time per launch with launches back to back (bench.py's measure)")
     return ap
 
 
@@ -222,11 +307,15 @@ def main(argv=None):
             row, pick, best, rho = study.summary(base)
             writer.writerow(row)
             fh.flush()
+            chosen = study.chosen(best)
             if not args.no_record:
-                record_best(args.tuned, args.workload, shape, best, pick, rho)
+                record_best(args.tuned, args.workload, shape, chosen, pick, rho, args.objective)
             print(f"{'x'.join(map(str, shape))}: model {pick.name} {pick.measured_ms:.4f} ms, best {best.name} "
                   f"{best.measured_ms:.4f} ms, ratio {best.measured_ms / pick.measured_ms:.3f}, spearman {rho:.3f}, "
                   f"{len(study.compiled())}/{len(study.candidates)} compiled", flush=True)
+            if args.objective == "throughput":
+                print(f"{'x'.join(map(str, shape))}: back to back {chosen.name} {chosen.window_ms:.4f} ms/launch "
+                      f"(per-launch median {chosen.measured_ms:.4f} ms)", flush=True)
     return 0
 
 

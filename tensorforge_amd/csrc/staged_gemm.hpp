@@ -144,6 +144,34 @@ struct StagedGemm {
   static constexpr int A_VECS = BM * BK / VW, B_VECS = BK * BN / VW;
   static constexpr int A_PER = (A_VECS + NT - 1) / NT, B_PER = (B_VECS + NT - 1) / NT;
 
+  // A staging vector q -> (row r, column c) of the BM x BK slab; thread tid
+  // stages q = tid + it * NT.  A 128-bit LDS write is served 8 lanes per
+  // cycle over 32 banks, so the 8 lanes of a pass must cover 8 distinct
+  // 4-bank groups; row r starts at group (r * LDA / 4) mod 8.  With BK >= 32
+  // a pass stays in one row (8 consecutive groups).  With BK = 16 a pass
+  // holds two whole rows, r and r + d with d * LDA / 4 = 4 mod 8 (d = 4 for
+  // LDA = 20, d = 2 for LDA = 24; consecutive rows share a group: 8 conflict
+  // cycles per write instruction, measured); with BK = 8 and LDA / 4 odd,
+  // four rows r, r + 2, r + 4, r + 6.  The rows of one wave's loads are the
+  // same 16 whole rows as with the row-major order, so global accesses
+  // coalesce as before.
+  static __device__ __forceinline__ void a_item(int q, int &r, int &c) {
+    constexpr int CPR = BK / VW, L = LDA / 4;
+    if constexpr (VEC && CPR == 4 && (L % 2 == 1 || L % 4 == 2)) {
+      const int s = q & 31, pass = s >> 3, i = s & 7;
+      const int base = L % 2 == 1 ? pass : (pass & 1) + 4 * (pass >> 1);
+      r = 8 * (q >> 5) + base + (L % 2 == 1 ? 4 : 2) * (i >> 2);
+      c = 4 * (i & 3);
+    } else if constexpr (VEC && CPR == 2 && L % 2 == 1) {
+      const int s = q & 15, i = s & 7;
+      r = 8 * (q >> 4) + (s >> 3) + 2 * (i >> 1);
+      c = 4 * (i & 1);
+    } else {
+      r = q / CPR;
+      c = (q - r * CPR) * VW;
+    }
+  }
+
   static_assert(BM % TM == 0 && BN % TN == 0, "block tile must be a multiple of the thread tile");
   static_assert(NWM * NWN * 64 == NT, "waves must tile the block");
   static_assert(WTM % 16 == 0 && WTN % 16 == 0, "wave tile must be made of 16x16 or 32x32 MFMA blocks");
@@ -240,7 +268,8 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
     const int Mi = p.M, Ni = p.N, Ki = p.K, m0i = (int)m0, n0i = (int)n0, kbi = (int)kbase;
     auto guarded = [&](int k0) __attribute__((always_inline)) { return MASK && (kbi + k0 + BK >= Ki || Ni < 4); };
     auto a_in = [&](int q, int k0, int e) __attribute__((always_inline)) {
-      const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
+      int r, c;
+      G::a_item(q, r, c);
       return m0i + r < Mi && kbi + k0 + c + e < Ki;
     };
     auto b_in = [&](int q, int k0, int e) __attribute__((always_inline)) {
@@ -284,7 +313,8 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
       return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), 0, 0x7fffffff, 0x00020000);
     };
     auto a_byte = [&](int it) __attribute__((always_inline)) {
-      const int q = tid + it * NT, r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
+      int r, c;
+      G::a_item(tid + it * NT, r, c);
       return (int)((r * lda + c) * 4);
     };
     auto b_byte = [&](int it) __attribute__((always_inline)) {
@@ -308,7 +338,8 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
         for (int it = 0; it < G::A_PER; ++it) {
           const int q = tid + it * NT;
           if (G::A_VECS % NT == 0 || q < G::A_VECS) {
-            const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
+            int r, c;
+            G::a_item(q, r, c);
             ra[set][it] = *reinterpret_cast<const VT *>(A + r * lda + k0 + c);
           }
         }
@@ -322,7 +353,8 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
         for (int it = 0; it < G::A_PER; ++it) {
           const int q = tid + it * NT;
           if (G::A_VECS % NT == 0 || q < G::A_VECS) {
-            const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
+            int r, c;
+            G::a_item(q, r, c);
             ra[set][it] = load16(p.A + (min(m0i + r, Mi - 1) * (int)lda + kbi + k0 + c));
           }
         }
@@ -338,7 +370,8 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
         for (int it = 0; it < G::A_PER; ++it) {
           const int q = tid + it * NT;
           if (G::A_VECS % NT == 0 || q < G::A_VECS) {
-            const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
+            int r, c;
+            G::a_item(q, r, c);
             const int base = (m0i + r) * (int)lda + kbi + k0 + c;
 #pragma unroll
             for (int e = 0; e < VW; ++e) put(ra[set][it], e, p.A[a_in(q, k0, e) ? base + e : 0]);
@@ -374,7 +407,8 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
       for (int it = 0; it < G::A_PER; ++it) {
         const int q = tid + it * NT;
         if (G::A_VECS % NT == 0 || q < G::A_VECS) {
-          const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
+          int r, c;
+          G::a_item(q, r, c);
           *reinterpret_cast<VT *>(&As[buf][r * LDA + c]) = ra[set][it];
         }
       }
@@ -435,7 +469,8 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
       } else if constexpr (it < G::A_PER) {
         const int q = tid + it * NT;
         if (G::A_VECS % NT == 0 || q < G::A_VECS) {
-          const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
+          int r, c;
+          G::a_item(q, r, c);
           if constexpr (!MASK) ra[set][it] = *reinterpret_cast<const VT *>(A + r * lda + k0 + c);
           else ra[set][it] = load16(p.A + (min(m0i + r, Mi - 1) * (int)lda + kbi + k0 + c));
         }
@@ -453,7 +488,8 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
       if constexpr (it < G::A_PER) {
         const int q = tid + it * NT;
         if (G::A_VECS % NT == 0 || q < G::A_VECS) {
-          const int r = q / (BK / VW), c = (q - r * (BK / VW)) * VW;
+          int r, c;
+          G::a_item(q, r, c);
           *reinterpret_cast<VT *>(&As[buf][r * LDA + c]) = ra[set][it];
         }
       } else {

@@ -95,8 +95,8 @@ streamed_gemm_kernel(GemmParams p) {
   int a_off[G::A_PER], b_off[G::B_PER], a_lds[G::A_PER], b_lds[G::B_PER];
 #pragma unroll
   for (int it = 0; it < G::A_PER; ++it) {
-    const int q = tid + it * NT;
-    const int r = q / (BK / 4), c = (q - r * (BK / 4)) * 4;
+    int r, c;
+    G::a_item(tid + it * NT, r, c);  // bank-conflict-free LDS writes
     a_off[it] = r * (int)lda + c;
     a_lds[it] = r * LDA + c;
   }
