@@ -299,14 +299,18 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
     // `gm` (std::integral_constant<int, 0 or 1>): 0 when the caller knows
     // the slab is not guarded (the masked kernels' steady state, see the slab
     // loop), so the guarded branch is not compiled in.
-    // Buffer loads (`bc` = BufOn; unmasked staging): the slab's base
-    // addresses go into two buffer resources (scalar 64-bit arithmetic) and
-    // each thread keeps one 32-bit byte offset per vector, so a global load
-    // carries no 64-bit vector address add.  Between the MFMAs of one wave per
+    // Buffer loads (`bc` = BufOn; unmasked staging, and the masked kernels'
+    // unguarded slabs): the slab's base addresses go into two buffer
+    // resources (scalar 64-bit arithmetic) and each thread keeps one 32-bit
+    // byte offset per vector, so a global load carries no 64-bit vector
+    // address add.  Between the MFMAs of one wave per
     // SIMD those adds cost 1.5 us at 1024^3 (64x64 t4x4 k16: 19.3 -> 17.75 us
     // back to back) and 6 us at 2048^3 (128x128 t8x8 k16: 126.4 -> 120.0 us).
     // Used only when every offset fits 31 bits (the caller checks BM * lda and
-    // BK * ldb); otherwise the same loop runs with flat loads.
+    // BK * ldb); otherwise the same loop runs with flat loads.  Masked
+    // kernels: A rows clamped to M - 1 as in their flat loads, offsets from
+    // the tile's first row; B columns are absolute (clamped to N - 4), so B's
+    // base is the slab's first row of the matrix.
     using BufOn = std::integral_constant<int, 1>;
     using BufOff = std::integral_constant<int, 0>;
     auto buf_rsrc = [](const float *base) __attribute__((always_inline)) {
@@ -315,24 +319,31 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
     auto a_byte = [&](int it) __attribute__((always_inline)) {
       int r, c;
       G::a_item(tid + it * NT, r, c);
+      if constexpr (MASK) r = min(m0i + r, Mi - 1) - m0i;
       return (int)((r * lda + c) * 4);
     };
     auto b_byte = [&](int it) __attribute__((always_inline)) {
+      if constexpr (MASK) return (b_off[it] - kbi * (int)ldb) * 4;
       const int q = tid + it * NT, r = q / (BN / VW), c = (q - r * (BN / VW)) * VW;
       return (int)((r * ldb + c) * 4);
+    };
+    auto b_base = [&](int k0) __attribute__((always_inline)) {
+      return MASK ? p.B + (kbase + k0) * ldb : B + (long)k0 * ldb;
+    };
+    auto buf_slab = [&](auto sc, int k0) __attribute__((always_inline)) {
+      constexpr int set = decltype(sc)::value;
+      const __amdgpu_buffer_rsrc_t rsa = buf_rsrc(A + k0), rsb = buf_rsrc(b_base(k0));
+#pragma unroll
+      for (int it = 0; it < G::A_PER; ++it)
+        if (G::A_VECS % NT == 0 || tid + it * NT < G::A_VECS) ra[set][it] = buffer_load_vt<VT>(rsa, a_byte(it));
+#pragma unroll
+      for (int it = 0; it < G::B_PER; ++it)
+        if (G::B_VECS % NT == 0 || tid + it * NT < G::B_VECS) rb[set][it] = buffer_load_vt<VT>(rsb, b_byte(it));
     };
     auto load_slab = [&](auto sc, auto gm, int k0, auto bc) __attribute__((always_inline)) {
       constexpr int set = decltype(sc)::value;
       if constexpr (!MASK && decltype(bc)::value) {
-        const __amdgpu_buffer_rsrc_t rsa = buf_rsrc(A + k0), rsb = buf_rsrc(B + (long)k0 * ldb);
-#pragma unroll
-        for (int it = 0; it < G::A_PER; ++it)
-          if (G::A_VECS % NT == 0 || tid + it * NT < G::A_VECS)
-            ra[set][it] = buffer_load_vt<VT>(rsa, a_byte(it));
-#pragma unroll
-        for (int it = 0; it < G::B_PER; ++it)
-          if (G::B_VECS % NT == 0 || tid + it * NT < G::B_VECS)
-            rb[set][it] = buffer_load_vt<VT>(rsb, b_byte(it));
+        buf_slab(sc, k0);
       } else if constexpr (!MASK) {
 #pragma unroll
         for (int it = 0; it < G::A_PER; ++it) {
@@ -349,6 +360,10 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
           if (G::B_VECS % NT == 0 || q < G::B_VECS) rb[set][it] = *reinterpret_cast<const VT *>(b_src[it] + k0 * ldb);
         }
       } else if (decltype(gm)::value == 0 || !guarded(k0)) {
+        if constexpr (decltype(bc)::value) {
+          buf_slab(sc, k0);
+          return;
+        }
 #pragma unroll
         for (int it = 0; it < G::A_PER; ++it) {
           const int q = tid + it * NT;
@@ -457,14 +472,14 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
     // guarded (the loads of load_slab's unmasked and unguarded paths).
     auto load_item = [&](auto sc, auto qc, int k0, auto bc) __attribute__((always_inline)) {
       constexpr int set = decltype(sc)::value, it = decltype(qc)::value;
-      if constexpr (!MASK && decltype(bc)::value) {
+      if constexpr (decltype(bc)::value) {
         if constexpr (it < G::A_PER) {
           if (G::A_VECS % NT == 0 || tid + it * NT < G::A_VECS)
             ra[set][it] = buffer_load_vt<VT>(buf_rsrc(A + k0), a_byte(it));
         } else {
           constexpr int ib = it - G::A_PER;
           if (G::B_VECS % NT == 0 || tid + ib * NT < G::B_VECS)
-            rb[set][ib] = buffer_load_vt<VT>(buf_rsrc(B + (long)k0 * ldb), b_byte(ib));
+            rb[set][ib] = buffer_load_vt<VT>(buf_rsrc(b_base(k0)), b_byte(ib));
         }
       } else if constexpr (it < G::A_PER) {
         const int q = tid + it * NT;
@@ -671,10 +686,12 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
     // block-staged ones with tiles of at least 128 x 128 (2048^3 t8x4 k32
     // 124.9 -> 123.6 us; the 8-wave 64x64 t4x2 k64 at 1024^3 was 2.4% slower
     // with them).  Not for 1024-thread workgroups (128 VGPRs per lane): the
-    // flat-load copy of the loop beside the buffer one spills there.
-    constexpr bool BUFCAP = !MASK && VEC && NT < 1024 && (SPREAD || BM * BN >= 128 * 128);
+    // flat-load copy of the loop beside the buffer one spills there; masked
+    // kernels only where they spread their staging (the block-staged masked
+    // ones with 512 threads and tile-k 32 or 64 spill with both loops).
+    constexpr bool BUFCAP = VEC && NT < 1024 && (SPREAD || (!MASK && BM * BN >= 128 * 128));
     if constexpr (BUFCAP) {
-      if ((long)BM * lda + BK < (1L << 29) && (long)BK * ldb + BN < (1L << 29)) k_loop(BufOn{});
+      if ((long)BM * lda + BK < (1L << 29) && (long)BK * ldb + (MASK ? Ni : BN) < (1L << 29)) k_loop(BufOn{});
       else k_loop(BufOff{});
     } else {
       k_loop(BufOff{});
