@@ -205,7 +205,10 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
   constexpr int LDA = G::LDA, LDB = G::LDB, VW = G::VW, MB = G::MB, KC = G::KC;
   using AccT = AccOf<MB>;
 
-  const int tid = threadIdx.y * blockDim.x + threadIdx.x;
+  // The block is (BN / TN) x (BM / TM) threads (launch_staged checks): with
+  // blockDim.x read from the dispatch packet instead, every wave waited for
+  // that load (~1.3k cycles) before its first global loads.
+  const int tid = threadIdx.y * (BN / TN) + threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / NWN, wn = wave - wm * NWN;
   const int lr = lane % MB, lg = lane / MB;  // row/column within a block, k group
@@ -819,6 +822,7 @@ staged_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int p
 
 template <int BM, int BN, int TM, int TN, int BK, int PROMOTE, int VEC, int MASK>
 hipError_t launch_staged(const GemmParams &p, dim3 grid, dim3 block, hipStream_t stream) {
+  if (block.x != BN / TN || block.y != BM / TM || block.z != 1) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL((staged_gemm_kernel<BM, BN, TM, TN, BK, PROMOTE, VEC, MASK>), grid, block, 0, stream, p.A, p.B,
                      p.lda, p.ldb, p.K, (int)grid.x, (int)grid.y, p.swizzle | (p.splits << 8), p.M, p.N, p);
   return hipGetLastError();

@@ -62,7 +62,7 @@ streamed_gemm_kernel(GemmParams p) {
   constexpr int LDA = G::LDA, LDB = G::LDB, MB = G::MB, KC = G::KC, LDC = S::LDC;
   using AccT = AccOf<MB>;
 
-  const int tid = threadIdx.y * blockDim.x + threadIdx.x;
+  const int tid = threadIdx.y * (BN / TN) + threadIdx.x;  // launch_streamed checks the block
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / NWN, wn = wave - wm * NWN;
   const int lr = lane % MB, lg = lane / MB;
@@ -377,6 +377,7 @@ streamed_gemm_kernel(GemmParams p) {
 
 template <int BM, int BN, int TM, int TN, int BK>
 hipError_t launch_streamed(const GemmParams &p, dim3 grid, dim3 block, hipStream_t stream) {
+  if (block.x != BN / TN || block.y != BM / TM || block.z != 1) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL((streamed_gemm_kernel<BM, BN, TM, TN, BK>), grid, block, 0, stream, p);
   return hipGetLastError();
 }

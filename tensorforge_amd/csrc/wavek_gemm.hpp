@@ -117,7 +117,10 @@ struct WaveKGemm {
 // The first eight arguments repeat the fields of `p` the prologue needs, as
 // scalars the hardware preloads into SGPRs (as for the staged kernels: the
 // library is built with kernel-argument preloading); gx, gy = gridDim.x, .y;
-// flags = swizzle | splits << 8.
+// flags = swizzle | splits << 8 | blockDim.x << 16: one instantiation serves
+// every thread tile with NT threads, so the block's width is an argument (a
+// preloaded one: blockDim.x from the dispatch packet made every wave wait for
+// that load, ~1.3k cycles, before its first global loads).
 template <int BM, int BN, int NT, int BK, int SB = wavek_stage_b<BM, BN>()>
 __global__ void __launch_bounds__(NT) wavek_gemm_kernel(const float *pA, const float *pB, long plda, long pldb, int pK,
                                                         int gx, int gy, int flags, GemmParams p) {
@@ -127,7 +130,8 @@ __global__ void __launch_bounds__(NT) wavek_gemm_kernel(const float *pA, const f
   p.ldb = pldb;
   p.K = pK;
   p.swizzle = flags & 255;
-  p.splits = flags >> 8;
+  p.splits = (flags >> 8) & 255;
+  const int bx = flags >> 16;
   using G = WaveKGemm<BM, BN, NT, BK, SB>;
   constexpr int W = G::W, MB = G::MB, KC = G::KC, C = G::C, FM = G::FM, FN = G::FN, NBUF = G::NBUF;
   constexpr int LDP = G::LDP, LDA = G::LDA, LPR = G::LPR, RPI = G::RPI, A_INSTR = G::A_INSTR;
@@ -136,7 +140,7 @@ __global__ void __launch_bounds__(NT) wavek_gemm_kernel(const float *pA, const f
   // Per-wave A staging tiles during the K loop, then the W partial tiles.
   __shared__ __attribute__((aligned(16))) float lds[G::LDS_BYTES / 4];
 
-  const int tid = threadIdx.y * blockDim.x + threadIdx.x;
+  const int tid = threadIdx.y * bx + threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane % MB, lg = lane / MB;
@@ -316,8 +320,9 @@ __global__ void __launch_bounds__(NT) wavek_gemm_kernel(const float *pA, const f
 
 template <int BM, int BN, int NT, int BK, int SB = wavek_stage_b<BM, BN>()>
 hipError_t launch_wavek(const GemmParams &p, dim3 grid, dim3 block, hipStream_t stream) {
+  if (block.x * block.y != NT || block.z != 1 || p.splits > 255) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL((wavek_gemm_kernel<BM, BN, NT, BK, SB>), grid, block, 0, stream, p.A, p.B, p.lda, p.ldb, p.K,
-                     (int)grid.x, (int)grid.y, p.swizzle | (p.splits << 8), p);
+                     (int)grid.x, (int)grid.y, p.swizzle | (p.splits << 8) | (int)(block.x << 16), p);
   return hipGetLastError();
 }
 
