@@ -399,6 +399,26 @@ def test_masked_edges_equal_pad_path_bits(workload, shape, cfg, extra):
     assert_bound(workload, ins, masked)
 
 
+@pytest.mark.parametrize("workload", ["mbr", "matmul"])
+@pytest.mark.parametrize("shape", [(130, 70, 91), (200, 300, 1010), (97, 130, 313), (65, 66, 109), (64, 64, 96)])
+@pytest.mark.parametrize("cfg", [(64, 64, 4, 4, 16), (128, 64, 8, 4, 16), (128, 128, 8, 8, 64)])
+def test_masked_k_tail_equals_pad_path_bits(workload, shape, cfg):
+    """The end of the K loop of masked kernels: the slab holding row K - 1 is
+    loaded element by element DEPTH slabs before it is stored with the zero
+    fill, after a steady loop of an even number of slabs.  Tile-k 16 (two
+    staging sets): K = 91, 1010, 313, 96, 109 give 6, 64, 20, 6, 7 slabs (an
+    even and an odd count after the steady loop); tile-k 64 (the 128 x 128
+    configuration, one staging set): 5, 16 and 2 slabs.  The pad path's bits
+    and the bound."""
+    m, n, k = shape
+    opts = STAGED.format(*cfg)
+    ins = o.make_inputs(workload, m, n, k)
+    _, masked = run_prog(workload, m, n, k, opts + " mask-edges=1", ins=ins)
+    _, padded = run_prog(workload, m, n, k, opts, ins=ins, logical=cm.padded(cfg, m, n, k))
+    assert o.bitwise_diff(masked, padded) == 0
+    assert_bound(workload, ins, masked)
+
+
 NARROW_SHAPES = [(5, 2, 3), (33, 3, 70), (70, 6, 9), (65, 7, 2), (2, 130, 5), (129, 1, 257)]
 
 
