@@ -155,7 +155,7 @@ struct StagedGemm {
   // four rows r, r + 2, r + 4, r + 6.  The rows of one wave's loads are the
   // same 16 whole rows as with the row-major order, so global accesses
   // coalesce as before.
-  static __device__ __forceinline__ void a_item(int q, int &r, int &c) {
+  static __host__ __device__ __forceinline__ void a_item(int q, int &r, int &c) {
     constexpr int CPR = BK / VW, L = LDA / 4;
     if constexpr (VEC && CPR == 4 && (L % 2 == 1 || L % 4 == 2)) {
       const int s = q & 31, pass = s >> 3, i = s & 7;
