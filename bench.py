@@ -382,7 +382,7 @@ def main():
                      "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": traffic,
                      "traffic_source": "profiles/traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)"
                      if traffic else None,
-                     "kernel_avg_ms": window_ms, "flop_per_launch": flops,
+                     "window_ms_per_launch": window_ms, "flop_per_launch": flops,
                      "per_launch_events": {"avg_ms": avg_ms, "median_ms": med_ms,
                                            "note": "each launch between its own event pair, after the window"}},
         "parity": parity, "autotune": autotune, "cpu_baseline": cpu,

@@ -40,8 +40,6 @@ extern "C" {
 #define TF_FAMILY_DIRECT 0      /* tile-k=0: one FMA chain per output          */
 #define TF_FAMILY_STAGED 1      /* tile-k>0: LDS-staged FP32 MFMA              */
 #define TF_FAMILY_ELEMENTWISE 2 /* programs without a matmul                   */
-#define TF_FAMILY_STREAMED 3    /* tile-k>0 with persistent: one workgroup per CU
-                                   streams K slabs over many output tiles      */
 #define TF_FAMILY_WAVEK 4       /* tile-k>0 with wave-split-k: the waves of a
                                    workgroup split K, partial tiles summed in
                                    LDS (one launch, no workspace)              */
@@ -122,14 +120,22 @@ int tf_device_info(tf_device_info_t *out);
  * launches and select the gfx950 instantiations.  No GPU work: runs on a host
  * without a GPU.  Replaces python/tforge_gpu.py:66-91 (compile_kernel's
  * tool chain).  Options are the reference's (include/TensorForge/Pipelines.h:45-72)
- * plus five backend options: split-k=S (S workgroups per output tile along K,
+ * plus four backend options: split-k=S (S workgroups per output tile along K,
  * then an ordered reduction launch), mask-edges (staged kernels accept shapes
- * that are not tile multiples), persistent (one workgroup per compute unit
- * works through many output tiles, writing each tile's C during the next
- * tile's matrix work; bit-identical to the same configuration without it),
- * wave-split-k (each wave of a workgroup reduces its own K range of the
- * workgroup's tile, the partial tiles are added in LDS in wave order: one
- * launch for shapes with few output tiles) and xcd-swizzle (default on). */
+ * that are not tile multiples), wave-split-k (each wave of a workgroup
+ * reduces its own K range of the workgroup's tile, the partial tiles are
+ * added in LDS in wave order: one launch for shapes with few output tiles)
+ * and xcd-swizzle (default on).
+ * Staged configurations (tile-k > 0) give each 64-lane wave an
+ * (8*TM) x (8*TN) output tile of MFMA blocks.  Where that wave tile cannot
+ * tile the block -- fewer than 64 threads, or a wave tile taller or wider
+ * than the block tile, as in 30 of the reference's 105 Stage 9
+ * configurations (python/costmodel.py:49-60) -- the same block tile and
+ * tile-k run on a stand-in wave layout: one wave over the whole block when
+ * there are fewer than 64 threads (thread tile BM/8 x BN/8), otherwise the
+ * same threads and accumulators per lane with the long side of the thread
+ * tile shortened to fit.  tf_kernel_launch_info then reports the block
+ * actually launched and the instantiation's name. */
 int tf_compile(const char *source_name, const char *program, const char *options, tf_kernel_t **out);
 void tf_kernel_free(tf_kernel_t *k);
 
@@ -177,7 +183,10 @@ int tf_launch(tf_kernel_t *k, void *const *device_buffers, void *stream);
  * with TF_E_ARG before anything is enqueued.  Nothing in the array needs
  * clearing between calls (every slice and intermediate is written whole
  * before it is read), but every call on one GPU shares it: calls that overlap
- * on that GPU -- from any handle or stream -- race, so serialise them. */
+ * on that GPU -- from any handle or stream -- race, so serialise them.
+ * `stream` must belong to the current device (TF_E_ARG otherwise).  The
+ * array's device address is looked up on the first call on each device; that
+ * first call may itself be under stream capture. */
 int tf_launch_noalloc(tf_kernel_t *k, void *const *device_buffers, void *stream);
 
 /* Correctness run, as the runner's "--warmup 0 --reps 1 --in-dir --out":
@@ -208,7 +217,9 @@ int tf_bench(tf_kernel_t *k, int mode, const long long *logical_mnk, const float
  * already queued on `stream` (a hipStream_t, NULL for the default stream)
  * counts shader-clock cycles against the 100 MHz wall clock in one workgroup
  * per XCD; mean, min and max over the XCDs (min/max may be NULL).
- * Synchronises the stream.  tf_bench takes one such sample after every rep;
+ * Synchronises the stream.  Each call writes its own result slot (64 slots
+ * per GPU, taken round robin), so calls from several threads or streams may
+ * overlap.  tf_bench takes one such sample after every rep;
  * the reference samples the SM clock through NVML instead
  * (runners/gpu/tforge-gpu-bench.cu:333-361). */
 int tf_clock_probe(void *stream, double *mean_mhz, double *min_mhz, double *max_mhz);

@@ -13,7 +13,7 @@ PKG = pathlib.Path(__file__).resolve().parent
 LIB_PATH = PKG / "libtforge_hip.so"
 
 TF_MODE_KERNEL, TF_MODE_BLAS = 0, 1
-FAMILY_NAMES = {0: "direct", 1: "staged", 2: "elementwise", 3: "streamed", 4: "wavek"}
+FAMILY_NAMES = {0: "direct", 1: "staged", 2: "elementwise", 4: "wavek"}
 
 
 class DeviceInfo(ctypes.Structure):

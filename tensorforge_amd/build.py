@@ -48,7 +48,7 @@ def _units():
     import gen_instances  # noqa: E402
     gen_instances.main()
     units = [CSRC / "runtime.hip", CSRC / "direct_kernels.hip", CSRC / "_gen" / "registry.hip",
-             CSRC / "_gen" / "streamed.hip", CSRC / "_gen" / "wavek.hip"]
+             CSRC / "_gen" / "wavek.hip"]
     units += sorted((CSRC / "_gen").glob("staged_*.hip"))
     return units
 
@@ -99,10 +99,6 @@ def _entry_name(demangled):
         bm, bn, tm, tn, bk, p, v, mk = m.groups()
         return (f"tf_staged_b{bm}x{bn}_t{tm}x{tn}_k{bk}" + ("" if p == "1" else "_noprom") +
                 ("" if v == "1" else "_novec") + ("_masked" if mk == "1" else ""))
-    m = re.search(r"streamed_gemm_kernel<(\d+), (\d+), (\d+), (\d+), (\d+)>", demangled)
-    if m:
-        bm, bn, tm, tn, bk = m.groups()
-        return f"tf_streamed_b{bm}x{bn}_t{tm}x{tn}_k{bk}"
     m = re.search(r"wavek_gemm_kernel<(\d+), (\d+), (\d+), (\d+)(?:, \d+)?>", demangled)
     if m:
         # One kernel serves every thread tile with its thread count.

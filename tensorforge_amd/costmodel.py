@@ -179,17 +179,34 @@ def name(cfg):
     return f"b{bm}x{bn}-t{tm}x{tn}-k{bk}" + ("-w" if wave_split_of(cfg) else "") + (f"-s{s}" if s > 1 else "")
 
 
+def kernel_tile(cfg):
+    """(TM, TN) of the instantiation that runs cfg: the option's thread tile,
+    or for a staged configuration whose (8 TM) x (8 TN) wave tile cannot tile
+    the block, the wave layout that stands in for it (csrc/gen_instances.py
+    wave_layout; the library reports that launch geometry)."""
+    bm, bn, tm, tn = cfg[:4]
+    if wave_split_of(cfg):
+        return tm, tn
+    return _gen_instances().wave_layout(bm, bn, tm, tn)
+
+
 def kernel_name(cfg):
-    bm, bn, tm, tn, bk = cfg[:5]
+    bm, bn, _, _, bk = cfg[:5]
+    tm, tn = kernel_tile(cfg)
     return f"tf_{'wavek' if wave_split_of(cfg) else 'staged'}_b{bm}x{bn}_t{tm}x{tn}_k{bk}"
 
 
+_GEN = []
+
+
 def _gen_instances():
-    import importlib.util
-    spec = importlib.util.spec_from_file_location("tf_gen_instances", PKG / "csrc" / "gen_instances.py")
-    mod = importlib.util.module_from_spec(spec)
-    spec.loader.exec_module(mod)
-    return mod
+    if not _GEN:
+        import importlib.util
+        spec = importlib.util.spec_from_file_location("tf_gen_instances", PKG / "csrc" / "gen_instances.py")
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        _GEN.append(mod)
+    return _GEN[0]
 
 
 def wave_split_space():
@@ -224,7 +241,8 @@ def estimate_info(cfg, target=MI355X, resources=None):
     """Blocks per CU without a GPU: the smaller of the register-limited waves
     per SIMD (compiler resource remarks) and the LDS limit; the occupancy API
     (tforge_gpu.info) gives the same number on the device."""
-    bm, bn, tm, tn, bk = cfg[:5]
+    bm, bn, _, _, bk = cfg[:5]
+    tm, tn = kernel_tile(cfg)
     threads = (bm // tm) * (bn // tn)
     w = threads // 64
     rec = (resources if resources is not None else _resources()).get(kernel_name(cfg), {})
@@ -263,9 +281,10 @@ def predict(cfg, padded, info, clock_mhz=None, target=MI355X):
                 "fma_step": fma_step, "lds_step": lds_step,
                 "bound": "dram" if t_dram > t_compute else ("smem" if lds_step > fma_step else "fma"),
                 "latency_exposed": exposed > 0, "intensity": 2.0 * bm * bn / (4.0 * (bm + bn))}
-    w = threads // 64
     if wave_split_of(cfg):
         return _predict_wave_split(cfg, padded, bps, blocks, waves, resident, clock, target)
+    tm, tn = kernel_tile(cfg)  # the launch geometry that runs cfg
+    w = (bm // tm) * (bn // tn) // 64
     mb = _block(tm, tn)
     fm, fn = 8 * tm // mb, 8 * tn // mb
     q = math.ceil(resident * w / target.simds)

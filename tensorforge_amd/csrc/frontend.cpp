@@ -576,8 +576,6 @@ bool parse_options(const std::string &text, Options &o, std::string &err) {
       if (!want_bool(o.xcd_swizzle)) return false;
     } else if (key == "mask-edges") {
       if (!want_bool(o.mask_edges)) return false;
-    } else if (key == "persistent") {
-      if (!want_bool(o.persistent)) return false;
     } else if (key == "wave-split-k") {
       if (!want_bool(o.wave_split_k)) return false;
     } else if (key == "block-tile" || key == "thread-tile") {

@@ -62,7 +62,6 @@ struct Options {
   bool xcd_swizzle = true;  // backend: XCD-aware tile order for staged kernels
   int64_t split_k = 1;      // backend: workgroups per output tile along K (staged kernels)
   bool mask_edges = false;  // backend: staged kernels take any shape (masked edge tiles, no padding)
-  bool persistent = false;  // backend: one workgroup per CU streams K slabs over its tiles (streamed kernel)
   bool wave_split_k = false;  // backend: the waves of a workgroup split K, partial tiles summed in LDS
   // Derived (reference lib/Pipelines/Pipelines.cpp:214-263).
   int64_t bm = 16, bn = 16, tm = 1, tn = 1;

@@ -9,7 +9,9 @@ The configuration space is the reference's Stage 9 grid (python/costmodel.py:49-
 BM, BN in {32, 64, 128}, TM x TN in {4x4, 8x4, 4x8, 8x8}, BK in {8, 16, 32}),
 widened for CDNA4 (BM, BN up to 256, BK up to 64), restricted to the
 configurations that map onto whole waves of 32x32 MFMA blocks, thread tiles
-2x2 / 2x4 / 4x2 on 16x16 MFMA blocks for small block tiles, plus the
+2x2 / 2x4 / 4x2 on 16x16 MFMA blocks for small block tiles, the wave layouts
+that run the reference grid's configurations whose own wave tile does not fit
+the block (wave_layout: 32x128 as 4x16, 128x32 as 16x4), plus the
 promote/vectorize ablation variants of the reference's Stage 8/9 ladders
 (bench/stage8_gpu.sh:7-14, bench/stage9_ablation.py:23-28), and a masked
 twin (any M, N, K; the mask-edges option) of every LDS-staged configuration.
@@ -48,6 +50,44 @@ def staged_valid(bm, bn, tm, tn, bk, promote=1):
     return None
 
 
+def wave_layout(bm, bn, tm, tn):
+    """The thread tile of the instantiation that runs block-tile=BM,BN
+    thread-tile=TM,TN (mirrors staged_wave_layout in runtime.hip): the
+    option's own, unless its (8*TM) x (8*TN) wave tile cannot tile the block
+    -- fewer than 64 threads: one wave owns the block (BM/8 x BN/8); a wave
+    tile taller or wider than the block: the same threads and accumulators
+    per lane with the long side shortened to fit."""
+    if bm % tm or bn % tn or bm % 8 or bn % 8:
+        return tm, tn
+    threads = (bm // tm) * (bn // tn)
+    ktm, ktn = tm, tn
+    if threads < 64:
+        ktm, ktn = bm // 8, bn // 8
+    elif 8 * tm > bm and (tm * tn) % (bm // 8) == 0:
+        ktm = bm // 8
+        ktn = tm * tn // ktm
+    elif 8 * tn > bn and (tm * tn) % (bn // 8) == 0:
+        ktn = bn // 8
+        ktm = tm * tn // ktn
+    if 8 * ktm > bm or 8 * ktn > bn or bm % ktm or bn % ktn:
+        return tm, tn
+    return ktm, ktn
+
+
+def reference_grid():
+    """The reference's Stage 9 grid (python/costmodel.py:49-60): 105 configurations."""
+    out = []
+    for bm in (32, 64, 128):
+        for bn in (32, 64, 128):
+            for tm, tn in ((4, 4), (8, 4), (4, 8), (8, 8)):
+                for bk in (8, 16, 32):
+                    threads = (bm // tm) * (bn // tn)
+                    if bm % tm or bn % tn or not 32 <= threads <= 1024:
+                        continue
+                    out.append((bm, bn, tm, tn, bk))
+    return out
+
+
 def configs():
     out = []
     for bm in (32, 64, 128, 256):
@@ -63,6 +103,12 @@ def configs():
                 for bk in (16, 32, 64):
                     if staged_valid(bm, bn, tm, tn, bk) is None:
                         out.append((bm, bn, tm, tn, bk, 1, 1))
+    # The wave layouts that stand in for the reference grid's configurations
+    # whose own wave tile cannot tile the block (wave_layout).
+    for bm, bn, tm, tn, bk in reference_grid():
+        c = (bm, bn) + wave_layout(bm, bn, tm, tn) + (bk, 1, 1)
+        if staged_valid(*c[:5]) is None and c not in out:
+            out.append(c)
     for bm, bn, tm, tn, bk in ((128, 64, 8, 4, 16), (64, 64, 4, 4, 16), (64, 64, 4, 4, 32),
                                (128, 128, 8, 8, 16), (128, 128, 8, 8, 8)):
         for promote, vec in ((0, 1), (1, 0), (0, 0)):
@@ -76,24 +122,6 @@ def configs():
 
 
 MASK_MAX_VECTORS = 16
-
-# Streamed (persistent) instantiations: the configurations that win on
-# problems with many tiles, whose LDS (A/B buffers, bias, and a whole C tile)
-# fits in 160 KiB.
-STREAMED = [(128, 128, 8, 4, 16), (128, 128, 8, 4, 32), (128, 128, 4, 4, 32), (128, 128, 8, 8, 32),
-            (64, 128, 4, 4, 32), (128, 64, 4, 4, 32), (64, 64, 4, 4, 32), (64, 128, 4, 4, 64),
-            (64, 64, 4, 2, 64), (64, 64, 2, 2, 64)]
-
-
-def streamed_lds(bm, bn, tm, tn, bk):
-    mb = 32 if (8 * tm) % 32 == 0 and (8 * tn) % 32 == 0 else 16
-    return (2 * (bm * (bk + (4 if mb == 32 else 8)) + bk * (bn + (8 if mb == 32 else 4))) + bn + bm * (bn + 4)) * 4
-
-
-def streamed_name(c):
-    bm, bn, tm, tn, bk = c
-    return f"tf_streamed_b{bm}x{bn}_t{tm}x{tn}_k{bk}"
-
 
 # Wave-split instantiations (the wave-split-k option): workgroup tiles with
 # few outputs, whose waves split K.  Keyed by (BM, BN, threads, BK); each
@@ -191,23 +219,6 @@ def main(shards=16):
         p = gen / f"staged_{i:02d}.hip"
         if not p.exists() or p.read_text() != text:
             p.write_text(text)
-    lines = ['#include "../streamed_gemm.hpp"', "", "namespace tfk {", "",
-             "#ifndef __HIP_DEVICE_COMPILE__  // host registry data", "extern const KernelEntry kStreamed[] = {"]
-    for c in STREAMED:
-        assert staged_valid(*c) is None and streamed_lds(*c) <= LDS_LIMIT, c
-        t = ", ".join(str(x) for x in c)
-        lines.append(f"    KernelEntry{{FAM_STREAMED, {t}, 1, 1, 0, \"{streamed_name(c)}\",")
-        lines.append(f"                reinterpret_cast<const void *>(&streamed_gemm_kernel<{t}>),")
-        lines.append(f"                &launch_streamed<{t}>, nullptr, StreamedGemm<{t}>::LDS_BYTES}},")
-    lines += ["};", f"extern const int kStreamedCount = {len(STREAMED)};", "#else",
-              "// Device pass: instantiate the kernels the host table names."]
-    for c in STREAMED:
-        lines.append(f"template __global__ void streamed_gemm_kernel<{', '.join(str(x) for x in c)}>(GemmParams);")
-    lines += ["#endif", "", "}  // namespace tfk", ""]
-    text = "\n".join(lines)
-    p = gen / "streamed.hip"
-    if not p.exists() or p.read_text() != text:
-        p.write_text(text)
     lines = ['#include "../wavek_gemm.hpp"', "", "namespace tfk {", "",
              "#ifndef __HIP_DEVICE_COMPILE__  // host registry data", "extern const KernelEntry kWaveK[] = {"]
     wk = wavek_configs()
@@ -231,7 +242,6 @@ def main(shards=16):
         p.write_text(text)
     reg = ['#include <vector>', '', '#include "../tf_kernels.h"', '', 'namespace tfk {', '',
            'extern const KernelEntry kDirectEntries[];', 'extern const int kDirectCount;',
-           'extern const KernelEntry kStreamed[];', 'extern const int kStreamedCount;',
            'extern const KernelEntry kWaveK[];', 'extern const int kWaveKCount;']
     for i in range(shards):
         reg += [f"extern const KernelEntry kStaged{i}[];", f"extern const int kStagedCount{i};"]
@@ -240,8 +250,7 @@ def main(shards=16):
             "    std::vector<KernelEntry> r(kDirectEntries, kDirectEntries + kDirectCount);"]
     for i in range(shards):
         reg.append(f"    r.insert(r.end(), kStaged{i}, kStaged{i} + kStagedCount{i});")
-    reg += ["    r.insert(r.end(), kStreamed, kStreamed + kStreamedCount);",
-            "    r.insert(r.end(), kWaveK, kWaveK + kWaveKCount);",
+    reg += ["    r.insert(r.end(), kWaveK, kWaveK + kWaveKCount);",
             "    return r;", "  }();", "  return v;", "}", "",
             "const KernelEntry *registry_begin() { return all_entries().data(); }",
             "const KernelEntry *registry_end() { return all_entries().data() + all_entries().size(); }",
@@ -250,7 +259,7 @@ def main(shards=16):
     p = gen / "registry.hip"
     if not p.exists() or p.read_text() != text:
         p.write_text(text)
-    print(f"{len(cfgs)} staged instantiations in {shards} shards, {len(STREAMED)} streamed, "
+    print(f"{len(cfgs)} staged instantiations in {shards} shards, "
           f"{len(wk)} wave-split ({n_entries} entries)")
 
 

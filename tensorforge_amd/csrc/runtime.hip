@@ -5,6 +5,7 @@
 #include <dlfcn.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -80,6 +81,38 @@ std::string staged_reason(long bm, long bn, long tm, long tn, long bk, bool prom
   return "no ahead-of-time instantiation of this configuration in libtforge_hip";
 }
 
+// The staged kernel gives each 64-lane wave an (8*TM) x (8*TN) output tile.
+// Where that wave tile cannot tile the block -- fewer than 64 threads (the
+// reference's 32-thread configurations such as block-tile=32,32
+// thread-tile=8,4), or a wave tile taller or wider than the block
+// (block-tile=32,64 thread-tile=8,4) -- the kernel runs the wave layout that
+// keeps the block tile and tile-k: with fewer than 64 threads one wave owns
+// the whole block (thread tile BM/8 x BN/8); otherwise the same number of
+// threads and accumulators per lane, with the thread tile's long side
+// shortened to fit (TM x TN = 8x4 on a 32-row block becomes 4x8).  ktm, ktn
+// receive the thread tile of the instantiation to run; they equal tm, tn
+// when the option's own layout fits.
+void staged_wave_layout(long bm, long bn, long tm, long tn, long &ktm, long &ktn) {
+  ktm = tm;
+  ktn = tn;
+  if (bm % tm || bn % tn || bm % 8 || bn % 8) return;
+  const long threads = (bm / tm) * (bn / tn);
+  if (threads < 64) {
+    ktm = bm / 8;
+    ktn = bn / 8;
+  } else if (8 * tm > bm && (tm * tn) % (bm / 8) == 0) {
+    ktm = bm / 8;
+    ktn = tm * tn / ktm;
+  } else if (8 * tn > bn && (tm * tn) % (bn / 8) == 0) {
+    ktn = bn / 8;
+    ktm = tm * tn / ktn;
+  }
+  if (8 * ktm > bm || 8 * ktn > bn || bm % ktm || bn % ktn) {
+    ktm = tm;
+    ktn = tn;
+  }
+}
+
 struct Launch {
   const tfk::KernelEntry *entry = nullptr;
   dim3 grid, block;
@@ -130,33 +163,22 @@ int select_launches(tf_kernel *k) {
       return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc,
                                                 "tforge-gpu-pipeline: mask-edges supports matrices below 2^31 "
                                                 "elements; pad this problem instead"));
-    // persistent: the streamed kernel for GEMM stages (element-op launches of
-    // an unfused program run as they are).
-    const bool streamed = o.persistent && gemm;
-    if (streamed) {
-      std::string why;
-      if (!staged) why = "persistent needs tile-k";
-      else if (masked) why = "persistent needs M, N and K to be multiples of the block and K tiles (pad the problem)";
-      else if (o.split_k > 1) why = "persistent and split-k exclude each other";
-      else if (!o.promote || !o.vectorize) why = "persistent needs promote=1 vectorize=1";
-      else if (st.K < 4 * o.tile_k || (st.K / o.tile_k) % 2) why = "persistent needs K to be an even number (at least 4) of tile-k slabs";
-      // The streamed kernel's per-thread staging offsets are 32-bit.
-      else if (o.bm * st.K >= (1L << 31) || o.tile_k * st.N >= (1L << 31)) why = "persistent supports BM*K and BK*N below 2^31";
-      if (!why.empty()) return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc, "tforge-gpu-pipeline: " + why));
-    }
     // wave-split-k: the wave-split kernel for GEMM stages.
     const bool wavek = o.wave_split_k && gemm;
     if (wavek) {
       std::string why;
       if (!staged) why = "wave-split-k needs tile-k";
       else if (masked) why = "wave-split-k needs M, N and K to be multiples of the block and K tiles (pad the problem)";
-      else if (o.persistent) why = "wave-split-k and persistent exclude each other";
-      else if (!o.vectorize) why = "wave-split-k needs vectorize=1";
+      else if (!o.promote || !o.vectorize) why = "wave-split-k needs promote=1 vectorize=1";
       // 32-bit buffer offsets from the tile's origin in A and in B.
       else if ((o.bm * st.K + st.K) * 4 >= (1L << 31) || (st.K * st.N + o.bn) * 4 >= (1L << 31))
         why = "wave-split-k supports (BM+1)*K and K*N below 2^29 elements";
       if (!why.empty()) return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc, "tforge-gpu-pipeline: " + why));
     }
+    // The staged kernel's thread tile: the option's own, or the wave layout
+    // that stands in for it when 8*TM x 8*TN waves cannot tile the block.
+    long ktm = o.tm, ktn = o.tn;
+    if (staged && !wavek) staged_wave_layout(o.bm, o.bn, o.tm, o.tn, ktm, ktn);
     for (const tfk::KernelEntry *e = tfk::registry_begin(); e != tfk::registry_end(); ++e) {
       if (wavek) {
         if (e->family == tfk::FAM_WAVEK && e->bm == o.bm && e->bn == o.bn && e->tm == o.tm && e->tn == o.tn &&
@@ -164,14 +186,8 @@ int select_launches(tf_kernel *k) {
           L.entry = e;
           break;
         }
-      } else if (streamed) {
-        if (e->family == tfk::FAM_STREAMED && e->bm == o.bm && e->bn == o.bn && e->tm == o.tm && e->tn == o.tn &&
-            e->bk == o.tile_k) {
-          L.entry = e;
-          break;
-        }
       } else if (staged) {
-        if (e->family == tfk::FAM_STAGED && e->bm == o.bm && e->bn == o.bn && e->tm == o.tm && e->tn == o.tn &&
+        if (e->family == tfk::FAM_STAGED && e->bm == o.bm && e->bn == o.bn && e->tm == ktm && e->tn == ktn &&
             e->bk == o.tile_k && e->promote == (int)o.promote && e->vectorize == (int)o.vectorize &&
             e->masked == masked) {
           L.entry = e;
@@ -186,7 +202,7 @@ int select_launches(tf_kernel *k) {
       }
     }
     if (!L.entry && masked) {
-      const long threads = (o.bm / o.tm) * (o.bn / o.tn);
+      const long threads = (o.bm / ktm) * (o.bn / ktn);
       const long vw = o.vectorize ? 4 : 1;
       const long vecs = (o.bm * o.tile_k / vw + threads - 1) / threads + (o.tile_k * o.bn / vw + threads - 1) / threads;
       if (vecs > 16)
@@ -201,25 +217,22 @@ int select_launches(tf_kernel *k) {
                                                 "tforge-gpu-pipeline: wave-split-k has no instantiation of this "
                                                 "configuration; wave-split configurations are listed by "
                                                 "tf_registry_entry"));
-    if (!L.entry && streamed)
-      return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc,
-                                                "tforge-gpu-pipeline: persistent has no instantiation of this "
-                                                "configuration (" + staged_reason(o.bm, o.bn, o.tm, o.tn, o.tile_k, true) +
-                                                "); streamed configurations are listed by tf_registry_entry"));
     if (!L.entry) {
-      std::string why = staged ? staged_reason(o.bm, o.bn, o.tm, o.tn, o.tile_k, o.promote)
+      std::string why = staged ? staged_reason(o.bm, o.bn, ktm, ktn, o.tile_k, o.promote)
                                : "thread-tile " + std::to_string(o.tm) + "," + std::to_string(o.tn) +
                                      " has no instantiation (1, 2, 4 or 8 per dimension)";
       return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc, "tforge-gpu-pipeline: " + why));
     }
-    const long tx = o.bn / o.tn, ty = o.bm / o.tm;
+    // The launch geometry is the instantiation's: (BN / TN, BM / TM) threads
+    // as in the reference (lib/Pipelines/Pipelines.cpp:139), with the
+    // stand-in thread tile where one replaced the option's.
+    const long tx = o.bn / ktn, ty = o.bm / ktm;
     if (tx * ty > 1024)
       return fail(TF_E_PLAN, tff::format_error(k->prog.source_name, st.loc,
                                                 "tforge-gpu-pipeline: " + std::to_string(tx * ty) +
                                                     " threads per block exceeds 1024"));
     L.block = dim3((unsigned)tx, (unsigned)ty, 1);
     L.grid = dim3((unsigned)std::max(1L, ceil_div(st.N, o.bn)), (unsigned)std::max(1L, ceil_div(st.M, o.bm)), 1);
-    if (streamed) L.grid = dim3((unsigned)std::min<long>(tfk::kStreamedGrid, (long)L.grid.x * L.grid.y), 1, 1);
     // split-k splits the K loop of GEMM stages; the element-op launches of an
     // unfused program run as they are.  Without tile-k it is an error.
     if (o.split_k > 1 && (gemm || o.tile_k == 0)) {
@@ -260,7 +273,7 @@ int launch_stage(const tf_kernel *k, size_t s, void *const *ptrs, void *ws, hipS
   if (st.M == 0 || st.N == 0) return TF_OK;
   // 128-bit accesses need 16-byte aligned buffers (the reference's ABI
   // guarantees 256-byte alignment: docs/stage8.md:34).
-  if (L.entry->family == tfk::FAM_STAGED || L.entry->family == tfk::FAM_STREAMED || L.entry->family == tfk::FAM_WAVEK) {
+  if (L.entry->family == tfk::FAM_STAGED || L.entry->family == tfk::FAM_WAVEK) {
     std::vector<int> ids = {st.a, st.b, st.out};
     for (const tff::EpiOp &e : st.epi)
       if (e.buf >= 0) ids.push_back(e.buf);
@@ -461,9 +474,14 @@ Stats stats(std::vector<double> v) {
 // Shader-clock probe: each workgroup (one per XCD: workgroups are dealt to the
 // 8 XCDs round-robin) spins for 4 us of the 100 MHz wall clock and records the
 // shader-clock cycles (s_memtime) that passed meanwhile.  The spin also ends
-// after 2^20 reads, so the kernel exits whatever the counters do.
+// after 2^20 reads, so the kernel exits whatever the counters do.  Each call
+// takes the next of kProbeSlots result slots (round robin), so up to that
+// many calls may run at once, from any threads and streams, without sharing
+// one.
 constexpr int kProbeGroups = 8;
-__device__ unsigned long long g_clock_probe[2 * kProbeGroups];
+constexpr int kProbeSlots = 64;
+__device__ unsigned long long g_clock_probe[kProbeSlots][2 * kProbeGroups];
+static std::atomic<unsigned> g_probe_next{0};
 
 __global__ void clock_probe_kernel(unsigned long long *out) {
   if (threadIdx.x != 0) return;
@@ -488,10 +506,11 @@ int clock_probe(hipStream_t stream, double &mean, double &mn, double &mx) {
     TF_HIP(hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, dev));
     probe_dev = dev;
   }
-  hipLaunchKernelGGL(clock_probe_kernel, dim3(kProbeGroups), dim3(64), 0, stream, probe_ptr);
+  unsigned long long *slot = probe_ptr + (size_t)(g_probe_next.fetch_add(1) % kProbeSlots) * 2 * kProbeGroups;
+  hipLaunchKernelGGL(clock_probe_kernel, dim3(kProbeGroups), dim3(64), 0, stream, slot);
   TF_HIP(hipGetLastError());
   unsigned long long h[2 * kProbeGroups];
-  TF_HIP(hipMemcpyAsync(h, probe_ptr, sizeof(h), hipMemcpyDeviceToHost, stream));
+  TF_HIP(hipMemcpyAsync(h, slot, sizeof(h), hipMemcpyDeviceToHost, stream));
   TF_HIP(hipStreamSynchronize(stream));
   mean = 0;
   mn = 1e30;
@@ -869,10 +888,19 @@ struct ScratchSlot {
 };
 static ScratchSlot g_scratch[kMaxDevices];
 
-// Device address of the current device's scratch array.
-static int scratch_base(void **out) {
+// Device address of the current device's scratch array.  `stream` must
+// belong to the current device: the kernels run on the stream's device, and
+// the address is that of the current device's copy.
+static int scratch_base(hipStream_t stream, void **out) {
   int dev = 0;
   TF_HIP(hipGetDevice(&dev));
+  if (stream) {
+    int sdev = dev;
+    TF_HIP(hipStreamGetDevice(stream, &sdev));
+    if (sdev != dev)
+      return fail(TF_E_ARG, "tf_launch_noalloc: the stream belongs to device " + std::to_string(sdev) +
+                                " but device " + std::to_string(dev) + " is current; make the stream's device current");
+  }
   if (dev < 0 || dev >= kMaxDevices) return fail(TF_E_ARG, "device " + std::to_string(dev) + " out of range");
   ScratchSlot &slot = g_scratch[dev];
   std::call_once(slot.once, [&] { slot.err = hipGetSymbolAddress(&slot.ptr, HIP_SYMBOL(scratch)); });
@@ -906,7 +934,7 @@ static int launch_noalloc_impl(tf_kernel_t *k, void *const *device_buffers, void
                           "intermediates); tf_launch_noalloc has " + std::to_string(kScratchBytes) +
                           " per GPU: use tf_launch, which allocates them");
   void *base = nullptr;
-  rc = scratch_base(&base);
+  rc = scratch_base(static_cast<hipStream_t>(stream), &base);
   if (rc) return rc;
   std::vector<void *> ptrs(pl.buffers.size(), nullptr);
   for (int i = 0; i <= pl.nargs; ++i) ptrs[i] = device_buffers[i];

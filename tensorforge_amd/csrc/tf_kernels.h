@@ -65,11 +65,7 @@ struct EltParams {
   int vec_ok;  // 1: every operand 16-byte aligned with row strides a multiple of 4
 };
 
-enum Family : int { FAM_DIRECT = 0, FAM_STAGED = 1, FAM_ELEMENTWISE = 2, FAM_STREAMED = 3, FAM_WAVEK = 4 };
-
-// Workgroups of a streamed (persistent) launch: one per MI355X compute unit,
-// or one per tile when there are fewer tiles.
-constexpr int kStreamedGrid = 256;
+enum Family : int { FAM_DIRECT = 0, FAM_STAGED = 1, FAM_ELEMENTWISE = 2, FAM_WAVEK = 4 };
 
 using GemmLauncher = hipError_t (*)(const GemmParams &, dim3 grid, dim3 block, hipStream_t);
 using EltLauncher = hipError_t (*)(const EltParams &, dim3 grid, dim3 block, hipStream_t);
@@ -77,7 +73,7 @@ using EltLauncher = hipError_t (*)(const EltParams &, dim3 grid, dim3 block, hip
 // One ahead-of-time instantiation of a kernel template.
 struct KernelEntry {
   int family;
-  int bm, bn, tm, tn, bk;  // staged, streamed, wave-split: full config; direct/elementwise: tm, tn only
+  int bm, bn, tm, tn, bk;  // staged, wave-split: full config; direct/elementwise: tm, tn only
   int promote, vectorize;
   int masked;  // staged: 1 = any M, N, K (edges masked in-kernel); 0 = tile multiples only
   const char *name;

@@ -244,8 +244,19 @@ def test_options_accept_braces_bools_and_print_script(capfd):
 
 
 def test_staged_config_without_waves_is_rejected():
-    err = compile_err(tc.gen_mlir("mbr", 64, 64, 64), "block-tile=32,32 thread-tile=8,4 tile-k=8 promote=1 vectorize=1")
+    """A block that is not a whole number of 64-lane waves and has no stand-in
+    wave layout (BM, BN not multiples of 8) is refused with the reason."""
+    err = compile_err(tc.gen_mlir("mbr", 72, 72, 64), "block-tile=36,36 thread-tile=6,6 tile-k=8 promote=1 vectorize=1")
     assert "not a whole number of 64-lane waves" in err
+
+
+def test_sub_wave_config_runs_on_one_wave():
+    """The reference's 32-thread block-tile=32,32 thread-tile=8,4 runs one
+    64-lane wave over the whole 32x32 block, and reports that block."""
+    k = _lib.Kernel(tc.gen_mlir("mbr", 64, 64, 64), "block-tile=32,32 thread-tile=8,4 tile-k=8 promote=1 vectorize=1")
+    launch = k.launches()[0]
+    assert launch["kernel"] == "tf_staged_b32x32_t4x4_k8"
+    assert launch["block"] == [8, 8, 1] and launch["grid"] == [2, 2, 1]
 
 
 def test_unfused_program_has_three_launches():

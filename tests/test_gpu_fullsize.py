@@ -15,6 +15,11 @@ therefore exact at any size, plus the reference's bound on sampled rows:
   * 32 sampled rows against the FP64 reference with the reference's bound
     (python/tforge_gpu.py:134-145) and exact ReLU masks, or the composed
     bound of the residual block.
+
+Inputs are the reference's seeded draws (numpy default_rng(1234) uniform[-1, 1]
+in the order a, b, bias: python/tforge_cpu.py:89-100; the residual block's
+standard-normal draws from tforge_cpu.make_inputs), made on the host and
+uploaded.
 """
 
 import numpy as np
@@ -52,10 +57,10 @@ def test_full_size_properties(workload, m, n, k):
     opts = cm.tuned_options(workload, m, n, k)
     kern = _lib.Kernel(tc.gen_mlir(workload, m, n, k), opts, "t.mlir")
     stream = torch.cuda.current_stream().cuda_stream
+    # The reference's seeded draws (numpy default_rng(1234), python/tforge_cpu.py:89-100).
+    host = o.make_inputs("mbr", m, n, k, seed=1234)
+    a, b, bias = (torch.from_numpy(host[s]).to(dev) for s in ("a", "b", "bias"))
     g = torch.Generator(device=dev).manual_seed(1234)
-    a = torch.rand(m, k, device=dev, generator=g) * 2 - 1
-    b = torch.rand(k, n, device=dev, generator=g) * 2 - 1
-    bias = torch.rand(n, device=dev, generator=g) * 2 - 1
     mbr = workload == "mbr"
 
     def run(a_, b_, bias_):
@@ -74,9 +79,9 @@ def test_full_size_properties(workload, m, n, k):
     assert torch.equal(_bits(run(a, b[:, cp], bias[cp])), _bits(out[:, cp]))
 
     rows = np.sort(np.random.default_rng(7).choice(m, size=min(32, m), replace=False))
-    ins = {"a": a[rows].cpu().numpy(), "b": b.cpu().numpy()}
+    ins = {"a": host["a"][rows], "b": host["b"]}
     if mbr:
-        ins["bias"] = bias.cpu().numpy()
+        ins["bias"] = host["bias"]
     got = out[rows].cpu().numpy()
     ref, bound = o.fp64_reference(workload, ins)
     assert o.e1_metrics(got, ref, bound)["max_err_over_bound"] <= 1.0

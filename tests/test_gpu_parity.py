@@ -109,13 +109,49 @@ def test_every_staged_instantiation():
     assert not failures, failures
 
 
-@pytest.mark.parametrize("opts", ["", STAGED.format(128, 128, 8, 8, 32)])
-def test_headline_2048(opts):
-    """The headline shape through the product's check() (reference bound), and
-    64 sampled rows of the same output against the oracle: the reference
-    bound and the ReLU-mask gate."""
-    d, launch = tg.compile_kernel("mbr", 2048, 2048, 2048, opts or "block-tile=16,16 thread-tile=1,1", tag="test")
+def test_reference_space_stand_in_layouts():
+    """The 30 configurations of the reference's Stage 9 grid whose own wave
+    tile cannot tile the block (python/costmodel.py:49-60) run on their
+    stand-in wave layout: each meets the reference bound with exact ReLU
+    masks on a padded problem and a ragged masked one, and equals, bit for
+    bit, the same problem run with the stand-in's own thread tile."""
+    shapes = {}
+    for cfg in cm.reference_space():
+        bm, bn, tm, tn, bk = cfg
+        ktm, ktn = cm.kernel_tile(cfg)
+        if (ktm, ktn) == (tm, tn):
+            continue
+        for masked in (False, True):
+            if masked and cfg in ((32, 128, 8, 8, 32), (128, 32, 8, 8, 32)):
+                continue  # no masked twin (20 staging vectors per thread)
+            m, n, k = (2 * bm - 3, 2 * bn - 5, 4 * bk - 7) if masked else (2 * bm, 2 * bn, 4 * bk)
+            if (m, n, k) not in shapes:
+                ins = o.make_inputs("mbr", m, n, k)
+                shapes[(m, n, k)] = (ins,) + o.fp64_reference("mbr", ins) + (o.preactivation64(ins),)
+            ins, ref, bound, z = shapes[(m, n, k)]
+            extra = " mask-edges=1" if masked else ""
+            print(f"stand-in {cfg} -> thread-tile {ktm},{ktn} at {m}x{n}x{k}{extra}", flush=True)
+            _, out = run_prog("mbr", m, n, k, cm.options(cfg) + extra, ins=ins)
+            assert not np.isnan(out).any()
+            assert o.e1_metrics(out, ref, bound)["max_err_over_bound"] <= 1.0, cfg
+            assert o.mask_mismatches(out, z, bound) == 0, cfg
+            _, own = run_prog("mbr", m, n, k, STAGED.format(bm, bn, ktm, ktn, bk) + extra, ins=ins)
+            assert o.bitwise_diff(out, own) == 0, cfg
+
+
+@pytest.mark.parametrize("which", ["naive", "tuned", "default"])
+def test_headline_2048(which):
+    """The headline shape through the product's check() (reference bound) with
+    the reference's default naive options, the autotuned configuration and the
+    cost model's pick, and 64 sampled rows of the same output against the
+    oracle: the reference bound and the ReLU-mask gate."""
+    opts = {"naive": "block-tile=16,16 thread-tile=1,1",
+            "tuned": cm.tuned_options("mbr", 2048, 2048, 2048),
+            "default": cm.options(cm.default_config(2048, 2048, 2048))}[which]
+    d, launch = tg.compile_kernel("mbr", 2048, 2048, 2048, opts, tag="test")
     res, out = tg.check("mbr", 2048, 2048, 2048, d, launch)
+    print(f"headline {which} {launch['kernel']}: err/bound {res['err_over_bound']:.5f} "
+          "(reference FMA kernels 0.00232, results/gpu/stage8.csv:86)", flush=True)
     assert res["pass"], res
     assert res["err_over_bound"] < 0.05
     ins = o.make_inputs("mbr", 2048, 2048, 2048)

@@ -237,35 +237,23 @@ def test_null_device_pointer_is_refused_before_any_launch():
     assert b"host input 0 is a null pointer" in L.tf_last_error()
 
 
-@pytest.mark.parametrize("shape,options,message", [
-    ((1000, 1024, 256), STAGED_16 + " mask-edges=1 persistent=1", "persistent needs M, N and K to be multiples"),
-    ((1024, 1024, 256), STAGED_16 + " split-k=2 persistent=1", "persistent and split-k exclude each other"),
-    ((1024, 1024, 256), "block-tile=16,16 thread-tile=1,1 persistent=1", "persistent needs tile-k"),
-    ((1024, 1024, 32), "block-tile=128,128 thread-tile=8,4 tile-k=16 promote=1 vectorize=1 persistent=1",
-     "persistent needs K to be an even number"),
-    ((1024, 1024, 160), "block-tile=128,128 thread-tile=8,4 tile-k=32 promote=1 vectorize=1 persistent=1",
-     "persistent needs K to be an even number"),
-    ((1024, 1024, 256), "block-tile=128,128 thread-tile=8,4 tile-k=32 promote=0 vectorize=1 persistent=1",
-     "persistent needs promote=1 vectorize=1"),
-    ((1024, 1024, 256), "block-tile=128,256 thread-tile=8,4 tile-k=32 promote=1 vectorize=1 persistent=1",
-     "persistent has no instantiation of this configuration"),
-])
-def test_persistent_option_refusals(shape, options, message):
-    """The persistent (streamed) option's limits are compile-time errors with
-    the reason (no GPU needed)."""
+def test_persistent_option_is_gone():
+    """The persistent (streamed) option was measured slower than the staged
+    kernel everywhere and removed; the option parser now refuses it like any
+    unknown option."""
     from tensorforge_amd import _lib
-    with pytest.raises(RuntimeError, match=message):
-        _lib.Kernel(tc.gen_mlir("mbr", *shape), options)
+    with pytest.raises(RuntimeError, match="no such option persistent"):
+        _lib.Kernel(tc.gen_mlir("mbr", 1024, 1024, 256), STAGED_16 + " persistent=1")
 
 
 @pytest.mark.parametrize("shape,options,message", [
     ((1000, 1024, 256), "block-tile=32,32 thread-tile=1,1 tile-k=32 promote=1 vectorize=1 mask-edges=1 "
      "wave-split-k=1", "wave-split-k needs M, N and K to be multiples"),
-    ((1024, 1024, 256), "block-tile=32,32 thread-tile=1,1 tile-k=32 promote=1 vectorize=1 wave-split-k=1 "
-     "persistent=1", "wave-split-k and persistent exclude each other"),
     ((1024, 1024, 256), "block-tile=16,16 thread-tile=1,1 wave-split-k=1", "wave-split-k needs tile-k"),
     ((1024, 1024, 256), "block-tile=32,32 thread-tile=1,1 tile-k=32 promote=1 vectorize=0 wave-split-k=1",
-     "wave-split-k needs vectorize=1"),
+     "wave-split-k needs promote=1 vectorize=1"),
+    ((1024, 1024, 256), "block-tile=32,32 thread-tile=1,1 tile-k=32 promote=0 vectorize=1 wave-split-k=1",
+     "wave-split-k needs promote=1 vectorize=1"),
     ((1024, 1024, 256), "block-tile=128,128 thread-tile=8,4 tile-k=32 promote=1 vectorize=1 wave-split-k=1",
      "wave-split-k has no instantiation of this configuration"),
     ((64, 65536, 16384), "block-tile=32,32 thread-tile=1,1 tile-k=32 promote=1 vectorize=1 wave-split-k=1",
@@ -303,12 +291,35 @@ def test_wave_split_configurations_in_the_cost_model():
         assert launch["kernel"] == cm.kernel_name(cfg)
 
 
-def test_persistent_launch_geometry():
-    """One workgroup per compute unit (256), or one per tile when fewer."""
+def test_reference_stage9_space_compiles():
+    """Every configuration of the reference's Stage 9 grid (105:
+    python/costmodel.py:49-60) compiles.  The 75 whose (8 TM) x (8 TN) wave
+    tile tiles the block run their own instantiation with the reference's
+    block (BN/TN, BM/TM); the other 30 run the stand-in wave layout and report
+    the block actually launched: one 64-lane wave over the whole block for
+    the 32-thread configurations, else the same thread count."""
     from tensorforge_amd import _lib
-    opts = "block-tile=128,128 thread-tile=8,4 tile-k=32 promote=1 vectorize=1 persistent=1"
-    big = _lib.Kernel(tc.gen_mlir("mbr", 4096, 4096, 256), opts).launches()[0]
-    assert big["family"] == "streamed" and big["grid"] == [256, 1, 1] and big["block"] == [32, 16, 1]
-    assert big["kernel"] == "tf_streamed_b128x128_t8x4_k32"
-    small = _lib.Kernel(tc.gen_mlir("mbr", 1024, 1024, 256), opts).launches()[0]
-    assert small["grid"] == [64, 1, 1]
+    from tensorforge_amd import costmodel as cm
+    ref = cm.reference_space()
+    assert len(ref) == 105
+    mapped = 0
+    for cfg in ref:
+        bm, bn, tm, tn, bk = cfg
+        for masked in (False, True):
+            if masked and cfg in ((32, 128, 8, 8, 32), (128, 32, 8, 8, 32)):
+                continue  # a 64-thread block staging 20 vectors per thread: no masked twin
+            shape = (2 * bm - 3, 2 * bn - 5, 4 * bk - 7) if masked else (2 * bm, 2 * bn, 4 * bk)
+            opts = cm.options(cfg) + (" mask-edges=1" if masked else "")
+            launch = _lib.Kernel(tc.gen_mlir("mbr", *shape), opts).launches()[0]
+            ktm, ktn = cm.kernel_tile(cfg)
+            assert launch["kernel"] == cm.kernel_name(cfg) + ("_masked" if masked else ""), (cfg, launch["kernel"])
+            assert launch["block"] == [bn // ktn, bm // ktm, 1]
+            assert launch["grid"][:2] == [-(-shape[1] // bn), -(-shape[0] // bm)]
+            threads = (bm // tm) * (bn // tn)
+            if (ktm, ktn) != (tm, tn):
+                mapped += not masked
+                assert (bn // ktn) * (bm // ktm) == max(threads, 64)
+                assert 8 * tm > bm or 8 * tn > bn or threads < 64
+    assert mapped == 30
+    with pytest.raises(RuntimeError, match="no masked twin|stage 20 vectors per slab"):
+        _lib.Kernel(tc.gen_mlir("mbr", 61, 251, 121), cm.options((32, 128, 8, 8, 32)) + " mask-edges=1")

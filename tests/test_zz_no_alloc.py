@@ -35,6 +35,41 @@ def _run(kern, bufs, out, noalloc, torch):
 
 
 @pytest.mark.gpu
+def test_noalloc_first_call_under_graph_capture():
+    """tf_launch_noalloc's first call in the process happens inside a HIP graph
+    capture (torch.cuda.graph), so the scratch array's address is looked up
+    there: a split-K mbr and the residual block (split-K workspace plus the
+    intermediate h), each graph replayed four times with eager work and a
+    synchronisation between replays, give tf_launch's eager bits every time.
+    (Runs first in this module: later tests have resolved the address.)"""
+    import torch
+    dev = torch.device("cuda:0")
+    for workload, (m, n, k), opts in [("mbr", (256, 1024, 2048), STAGED + " split-k=4"),
+                                      ("resmlp", (256, 512, 1024), STAGED + " split-k=2")]:
+        print(f"noalloc under capture {workload} {m}x{n}x{k} [{opts}]", flush=True)
+        ins = tc.make_inputs(workload, m, n, k)
+        bufs = [torch.from_numpy(np.ascontiguousarray(v)).to(dev) for v in ins.values()]
+        out = torch.empty((m, n), device=dev, dtype=torch.float32)
+        kern = _lib.Kernel(tc.gen_mlir(workload, m, n, k), opts, "noalloc.mlir")
+        want = _run(kern, bufs, out, False, torch)
+        ptrs = [b.data_ptr() for b in bufs] + [out.data_ptr()]
+        graph = torch.cuda.CUDAGraph()
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            kern.launch_noalloc(ptrs, torch.cuda.current_stream().cuda_stream)
+        for replay in range(4):
+            out.fill_(float("nan"))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            got = out.cpu().numpy()
+            assert not np.isnan(got).any(), (workload, replay)
+            assert o.bitwise_diff(got, want) == 0, (workload, replay)
+        del graph
+
+
+@pytest.mark.gpu
 def test_noalloc_matches_tf_launch_on_consecutive_calls():
     import torch
     dev = torch.device("cuda:0")
