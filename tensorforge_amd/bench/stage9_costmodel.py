@@ -245,9 +245,12 @@ class ShapeStudy:
         return row, pick, best, float(rho)
 
 
-def record_best(path, workload, shape, best, pick, rho, objective="latency"):
+def record_best(path, workload, shape, best, pick, rho, objective="latency", source=None):
     """Records `best` for (workload, shape).  "tflops" is at the objective's
-    time: the per-launch median, or the back-to-back time (window_ms)."""
+    time: the per-launch median, or the back-to-back time (window_ms).
+    `source` names the run behind the entry -- the commit the library was
+    built from, the date and the summary file whose row (commit, date, shape)
+    this study wrote -- so every recorded configuration traces to a row."""
     path = pathlib.Path(path)
     table = json.loads(path.read_text()) if path.exists() else {}
     m, n, k = shape
@@ -257,16 +260,29 @@ def record_best(path, workload, shape, best, pick, rho, objective="latency"):
         "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12, "model_pick": pick.name,
         "model_pick_ms": pick.measured_ms, "speedup_over_model_pick": pick.measured_ms / best.measured_ms,
         "spearman": rho, "objective": objective}
+    if source:
+        entry.update(source)
     if objective == "throughput":
         entry["back_to_back_ms"] = best.window_ms
     table[f"{workload}/{m}x{n}x{k}"] = entry
     path.write_text(json.dumps(table, indent=1, sort_keys=True) + "\n")
 
 
+def default_summary(workload, space):
+    """One summary file per workload and space, each with the reference's
+    columns (bench/stage9_costmodel.py:58-61), so rows of different studies
+    of one shape are never mixed."""
+    name = "stage9_summary" + ("" if workload == "mbr" else f"_{workload}") + \
+        ("" if space == "cdna4" else "_reference_space")
+    return f"results/gpu/{name}.csv"
+
+
 def cli():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--csv", default="results/gpu/stage9_autotune.csv")
-    ap.add_argument("--summary", default="results/gpu/stage9_summary.csv")
+    ap.add_argument("--summary", default=None,
+                    help="summary CSV (the reference's columns); default results/gpu/stage9_summary.csv for mbr "
+                         "over the CDNA4 space, with _matmul and/or _reference_space before .csv otherwise")
     ap.add_argument("--shapes", default="")
     ap.add_argument("--workload", default="mbr", choices=harness.GEMM_WORKLOADS)
     ap.add_argument("--warmup", type=int, default=10)
@@ -290,7 +306,7 @@ def main(argv=None):
     args = cli().parse_args(argv)
     table = provenance.ResultsTable(args.csv)
     base = table.base
-    summary_path = pathlib.Path(args.summary)
+    summary_path = pathlib.Path(args.summary or default_summary(args.workload, args.space))
     summary_path.parent.mkdir(parents=True, exist_ok=True)
     fresh = not summary_path.exists() or summary_path.stat().st_size == 0
     with open(summary_path, "a", newline="") as fh:
@@ -309,7 +325,9 @@ def main(argv=None):
             fh.flush()
             chosen = study.chosen(best)
             if not args.no_record:
-                record_best(args.tuned, args.workload, shape, chosen, pick, rho, args.objective)
+                source = {"commit": base["commit"], "date": base["date"], "summary": str(summary_path),
+                          "summary_row": f"{base['commit']},{base['job_id']},{base['date']},{'x'.join(map(str, shape))}"}
+                record_best(args.tuned, args.workload, shape, chosen, pick, rho, args.objective, source)
             print(f"{'x'.join(map(str, shape))}: model {pick.name} {pick.measured_ms:.4f} ms, best {best.name} "
                   f"{best.measured_ms:.4f} ms, ratio {best.measured_ms / pick.measured_ms:.3f}, spearman {rho:.3f}, "
                   f"{len(study.compiled())}/{len(study.candidates)} compiled", flush=True)

@@ -17,21 +17,34 @@ replaces the per-step terms with what bounds the gfx950 MFMA kernel:
 
   mfma_step  FP32 MFMA issue on the busiest SIMD: the resident waves share 4
              SIMDs (q = ceil(resident * W / 4) waves per SIMD), and a wave's
-             slab is FM*FN*(BK/2) v_mfma_f32_32x32x2 of 64 cycles each.
+             slab is FM*FN*(BK/2) v_mfma_f32_32x32x2 of 64 cycles each,
+             divided by the kernel structure's efficiency (below).
   lds_step   LDS bytes per slab over 128 B/clk: per wave (BK/8)*1 KiB per
              32-row A block (b128 reads) and per 32-column B block (b32
              reads), plus the block's (BM+BN)*BK*4 B of stores.
   l2_step    global -> LDS bytes per slab, (BM+BN)*BK*4 per block, over the
-             L2 bandwidth share of a CU (64 B/clk).
-  exposed    the next slab's loads are in flight during the current slab
-             (double buffering): max(0, LATENCY - compute) is exposed.
-  sync       one barrier per slab; its bubble is hidden by other waves on the
-             SIMD, so it is divided by q.
+             rate one CU streams from L2: ~22 B/clk, set by the L2 requests a
+             CU keeps in flight (~60 at ~340 cycles, measured), not by the
+             64 B/clk fill bandwidth -- small tiles at one or two workgroups
+             per CU are bound by it.
+  exposed    the loads of a slab are issued DEPTH slabs before its LDS write
+             (two register staging sets where a thread stages at most 8
+             vectors per slab, else one set, 1.5 slabs ahead), so
+             max(0, LATENCY - DEPTH * compute) is exposed per slab.
+  sync       one barrier per slab; measured to cost nothing visible in the
+             launch time (the waves' MFMAs cover it), so 0.
+  efficiency of the kernel structure (calibrated on the Stage 9 measurements):
+             16x16 MFMA blocks (v_mfma_f32_16x16x4_f32: twice the
+             instructions and fragment reads per FLOP) and block-staged
+             kernels (the staging burst between two chunks of MFMAs, rather
+             than one staging operation after each MFMA) each run at 1/1.05
+             of the MFMA rate.
 
 Split-K (a backend option, a sixth configuration entry S): S workgroups per
 output tile, each over Kp/S; the tile count is multiplied by S and the K
 steps divided by S, and the reduction launch adds its HBM traffic (S partial
-slices written and read, C written) plus a fixed launch cost.
+slices written and read, C written; at least the shortest measured
+reduction kernel) plus a fixed launch cost.
 
 Wave-split (the wave-split-k backend option, a seventh configuration entry
 1): the waves of a workgroup split its K range and add their partial tiles in
@@ -44,8 +57,16 @@ model takes the larger of that stream and the MFMA time per CU, plus the LDS
 round trip of the staged A (and B) slabs and the final partial-tile sum.
 
 Constants are AMD's published MI355X figures (256 CUs, 2.4 GHz, FP32 matrix
-256 FLOP/clk/CU, 160 KiB LDS, 8 TB/s HBM); LATENCY and SYNC are assumptions
-calibrated on measurements, and the model only ranks configurations.
+256 FLOP/clk/CU, 160 KiB LDS, 8 TB/s HBM) and measured ones (the per-CU L2
+stream, the shortest reduction kernel); LATENCY, the structure divisor 1.05
+and the wave-split big-tile efficiency 0.55 (from the 64 x 4096 x 4096
+measurements, where the wave-split family is the one that matters) are
+calibrated on the Stage 9 measurements, and the model only ranks
+configurations.  Over the 22 (workload, shape) studies of the tuned shapes
+its pick reached 0.90-1.00 of the measured best (mean 0.987); the terms that
+moved it there from 0.82-1.00 are the L2 stream rate for small tiles, the
+staging depth in the exposed latency, the first-slab prologue and the
+structure divisor.
 """
 
 import dataclasses
@@ -69,13 +90,16 @@ class Target:
     latency: float = 600.0              # cycles, global load missing L1
     lds_bytes_per_cycle: float = 128.0  # mfma
     l2_bytes_per_cycle: float = 64.0    # mfma, per CU
-    sync: float = 160.0                 # mfma, barrier bubble per slab
+    sync: float = 0.0                   # mfma, barrier bubble per slab
     simds: int = 4
     mfma_cycles: float = 64.0           # v_mfma_f32_32x32x2_f32 per wave
     lds_per_cu: int = 160 * 1024
     max_waves_per_simd: int = 8
     launch_s: float = 3e-6              # mfma: one more dependent kernel launch (split-K reduction)
-    l2_stream_bytes_per_cycle: float = 22.0  # mfma: measured per-CU L2 -> register stream (wave-split)
+    reduce_min_s: float = 2.5e-6        # mfma: shortest reduction kernel (measured 3.3-4.0 us at 64 x 4096)
+    l2_stream_bytes_per_cycle: float = 22.0  # mfma: measured per-CU L2 -> CU stream (L2 requests in flight)
+    slow_structure: float = 1.05        # mfma: MFMA-rate divisor for 16x16 blocks and for block staging
+    wave_split_big_tile: float = 0.55   # mfma: MFMA efficiency of wave-split tiles of >= 4 32x32 blocks
 
 
 # The reference's model (python/costmodel.py:41-46); TF_GPU_SMS / TF_GPU_DRAM_BW as there.
@@ -112,6 +136,22 @@ def _wave_lds_bytes(bm, bn, w, bk):
     mb = 32 if bm % 32 == 0 and bn % 32 == 0 else 16
     stage = bm * (bk + (4 if mb == 32 else 8)) + (0 if mb == 32 else bk * (bn + 4))
     return w * max(stage, bm * (bn + 4)) * 4
+
+
+def _staging(bm, bn, tm, tn, bk):
+    """(DEPTH, spread) of the staged kernel (csrc/staged_gemm.hpp): two register
+    staging sets (loads two slabs ahead) where a thread stages at most 8
+    vectors per slab, else one; the staging spread over the MFMAs for
+    workgroups of at most 256 threads with two sets and at least two
+    k-chunks per slab that have room for it."""
+    mb = _block(tm, tn)
+    nt = (bm // tm) * (bn // tn)
+    fm, fn = 8 * tm // mb, 8 * tn // mb
+    vec = -(-(bm * bk // 4) // nt) + -(-(bk * bn // 4) // nt)
+    depth = 2 if vec <= 8 else 1
+    chunks = bk // (256 // mb)
+    spread = nt <= 256 and depth == 2 and chunks >= 2 and 2 * vec <= 4 * fm * fn * (chunks - 1)
+    return depth, spread
 
 
 def _lds_bytes(bm, bn, tm, tn, bk):
@@ -287,25 +327,29 @@ def predict(cfg, padded, info, clock_mhz=None, target=MI355X):
     w = (bm // tm) * (bn // tn) // 64
     mb = _block(tm, tn)
     fm, fn = 8 * tm // mb, 8 * tn // mb
+    depth, spread = _staging(bm, bn, tm, tn, bk)
     q = math.ceil(resident * w / target.simds)
     # FP32 MFMA: 64 FLOP per SIMD clock for both block sizes (4096 FLOP in 64
     # cycles, or 2048 in 32); a wave's slab is 2 * (8 TM)(8 TN) BK FLOP.
-    mfma_step = q * 2 * (8 * tm) * (8 * tn) * bk / 64.0 * (target.mfma_cycles / 64.0)
+    slow = (target.slow_structure if mb == 16 else 1.0) * (1.0 if spread else target.slow_structure)
+    mfma_step = q * 2 * (8 * tm) * (8 * tn) * bk / 64.0 * (target.mfma_cycles / 64.0) * slow
     # per chunk of 256 / mb k values, 1 KiB per A block-row and per B block-column
     lds_bytes = resident * (w * (bk / (256 // mb)) * 1024 * (fm + fn) + (bm + bn) * bk * 4)
     lds_step = lds_bytes / target.lds_bytes_per_cycle
-    l2_step = resident * (bm + bn) * bk * 4 / target.l2_bytes_per_cycle
+    l2_step = resident * (bm + bn) * bk * 4 / target.l2_stream_bytes_per_cycle
     compute = max(mfma_step, lds_step, l2_step)
-    exposed = max(0.0, target.latency - compute)
+    exposed = max(0.0, target.latency - (2.0 if depth == 2 else 1.5) * compute)
     step = compute + exposed + target.sync / q
     epilogue = target.latency + resident * bm * bn * 4 / target.l2_bytes_per_cycle
+    # the first slab of every resident workgroup arrives before any MFMA
+    prologue = target.latency + resident * (bm + bn) * bk * 4 / target.l2_stream_bytes_per_cycle
     ksteps = -(-(kp // bk) // splits)
-    cycles = waves * (ksteps * step + target.latency + epilogue)
+    cycles = waves * (ksteps * step + prologue + epilogue)
     t_compute = cycles / (clock * 1e6)
     t_dram = 4.0 * (mp * kp + kp * np_ + mp * np_ + np_) / target.dram_bw
     t = max(t_compute, t_dram)
     if splits > 1:
-        t += (2 * splits + 1) * 4.0 * mp * np_ / target.dram_bw + target.launch_s
+        t += max((2 * splits + 1) * 4.0 * mp * np_ / target.dram_bw, target.reduce_min_s) + target.launch_s
     terms = {"mfma": mfma_step, "lds": lds_step, "l2": l2_step}
     bound = "dram" if t_dram > t_compute else max(terms, key=terms.get)
     return {"pred_ms": t * 1e3, "waves": waves, "resident": resident, "blocks": blocks,
@@ -324,6 +368,8 @@ def _predict_wave_split(cfg, padded, bps, blocks, waves, resident, clock, target
     w = (bm // tm) * (bn // tn) // 64
     kz = kp / splits
     mfma = resident * 2.0 * bm * bn * kz / (target.simds * 64.0)
+    if (bm // 32) * (bn // 32) >= 4:  # a 64x64 tile per wave: measured at about half the MFMA rate
+        mfma /= target.wave_split_big_tile
     l2 = resident * (bm + bn) * kz * 4 / target.l2_stream_bytes_per_cycle
     mb = 32 if bm % 32 == 0 and bn % 32 == 0 else 16
     staged = bm + (0 if mb == 32 else bn)
@@ -334,7 +380,7 @@ def _predict_wave_split(cfg, padded, bps, blocks, waves, resident, clock, target
     t_dram = 4.0 * (mp * kp + kp * np_ + mp * np_ + np_) / target.dram_bw
     t = max(t_compute, t_dram)
     if splits > 1:
-        t += (2 * splits + 1) * 4.0 * mp * np_ / target.dram_bw + target.launch_s
+        t += max((2 * splits + 1) * 4.0 * mp * np_ / target.dram_bw, target.reduce_min_s) + target.launch_s
     terms = {"mfma": mfma, "lds": lds, "l2": l2}
     bound = "dram" if t_dram > t_compute else max(terms, key=terms.get)
     return {"pred_ms": t * 1e3, "waves": waves, "resident": resident, "blocks": blocks,
