@@ -325,7 +325,7 @@ def main(argv=None):
             fh.flush()
             chosen = study.chosen(best)
             if not args.no_record:
-                source = {"commit": base["commit"], "date": base["date"], "summary": str(summary_path),
+                source = {"commit": base["commit"], "date": base["date"], "summary": summary_path.name,
                           "summary_row": f"{base['commit']},{base['job_id']},{base['date']},{'x'.join(map(str, shape))}"}
                 record_best(args.tuned, args.workload, shape, chosen, pick, rho, args.objective, source)
             print(f"{'x'.join(map(str, shape))}: model {pick.name} {pick.measured_ms:.4f} ms, best {best.name} "
