@@ -17,7 +17,8 @@ and fills it in three passes:
   throughput  (--objective throughput) every timed configuration's rate with
             launches issued back to back, as bench.py measures its value:
             one window of 50 launches after 10 untimed ones, then the six
-            best alternate in six rounds and their median windows decide
+            best alternate in ten rounds of ~25 ms windows (20-200 launches)
+            and their median windows decide
 
 and then compares: the model's pick (least predicted time, passing) against
 the measured best, raw and clock-adjusted; each one's rank in the other's
@@ -135,11 +136,13 @@ class ShapeStudy:
             print(f"  {c.name:>18} {c.measured_ms:.4f} ms {c.result.rate()[1] / 1e3:7.2f} TFLOP/s  "
                   f"pred {c.pred['pred_ms']:.4f} ms", flush=True)
 
-    def throughput(self, warm=10, steps=50, finalists=6, rounds=6):
+    def throughput(self, warm=10, steps=50, finalists=6, rounds=10, final_window_s=0.025):
         """Back-to-back ms per launch of every timed candidate (one window of
         `steps` launches after `warm` untimed ones), then of the `finalists`
         best again over `rounds` alternating rounds (first to last, then last
-        to first), each candidate's median window.  Inputs are uniform [-1, 1]
+        to first), each candidate's median window; a final window spans about
+        `final_window_s` of launches (20 to 200), since finalists lie within
+        a percent of each other.  Inputs are uniform [-1, 1]
         device buffers of the shapes the kernel takes; launches go straight to
         tf_launch, so the host issues them faster than the shortest kernel
         here runs."""
@@ -178,11 +181,12 @@ class ShapeStudy:
             c.window_ms = window(steps)
         final = sorted(pool, key=lambda c: c.window_ms)[:finalists]
         times = {c.name: [] for c in final}
+        long_steps = max(20, min(200, int(final_window_s / (final[0].window_ms * 1e-3))))
         for r in range(rounds):
             for c in (final if r % 2 == 0 else final[::-1]):
                 _, window = launchers[c.name]
                 window(warm)
-                times[c.name].append(window(steps))
+                times[c.name].append(window(long_steps))
         for c in final:
             c.window_ms = statistics.median(times[c.name])
             print(f"  {c.name:>18} back to back {c.window_ms * 1e3:.1f} us/launch "
