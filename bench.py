@@ -152,6 +152,10 @@ def parity_sample(torch, A, B, bias, C, rows=64):
             "pass": eob <= 1.0 and masks == 0 and not bool(torch.isnan(out).any())}
 
 
+# The reference's Stage 8 headline tiles (ref:results/gpu/stage8.csv:86; ref:bench/stage8_gpu.sh).
+REFERENCE_TILES = "block-tile=128,64 thread-tile=8,4 tile-k=16 promote=1 vectorize=1"
+
+
 def interleaved(launchers, rounds=6, steps=50, warm=10):
     """Median ms per launch of each launcher over `rounds` alternating rounds
     (the first launcher leads in even rounds, the last in odd ones), each
@@ -343,16 +347,35 @@ def main():
         f"{avg_ms * 1e3:.1f} / median {med_ms * 1e3:.1f} us, clock {clock_mhz[0]:.0f} MHz, parity {parity}")
 
     autotune = None
-    if not args.no_autotune_compare and opts != dflt:
-        kd = _lib.Kernel(program, dflt, "bench.mlir")
-        med, _ = interleaved({"selected": run, "default": Launcher(kd, ptrs, stream, torch)})
-        default_parity = parity_sample(torch, A, B, bias, C)  # C holds the default's output now
-        autotune = {"default_options": dflt, "selected_options": opts,
-                    "default_tflops": flops / (med["default"] * 1e-3) / 1e12,
-                    "selected_tflops": flops / (med["selected"] * 1e-3) / 1e12,
-                    "speedup_over_default": med["default"] / med["selected"],
+    if not args.no_autotune_compare:
+        # The autotuned configuration against the cost model's pick, and both
+        # against the reference's own Stage 8 tiles (ref:results/gpu/stage8.csv:86,
+        # full-128x64-t8x4-k16) run on this backend, in alternating rounds.
+        others = {"default": dflt, "reference_tiles": REFERENCE_TILES}
+        others = {k: v for k, v in others.items() if v != opts}
+        if "default" in others and others.get("reference_tiles") == dflt:
+            del others["reference_tiles"]
+        launchers = {"selected": run}
+        launchers.update({k: Launcher(_lib.Kernel(program, v, "bench.mlir"), ptrs, stream, torch) for k, v in others.items()})
+        med, _ = interleaved(launchers)
+        tf = {k: flops / (ms * 1e-3) / 1e12 for k, ms in med.items()}
+        default_parity = parity
+        if "default" in others:
+            Launcher(_lib.Kernel(program, dflt, "bench.mlir"), ptrs, stream, torch).launch(1)
+            torch.cuda.synchronize()
+            default_parity = parity_sample(torch, A, B, bias, C)  # C holds the default's output now
+        autotune = {"default_options": dflt, "selected_options": opts, "reference_tiles_options": REFERENCE_TILES,
+                    "selected_tflops": tf["selected"],
+                    "default_tflops": tf.get("default", tf["selected"]),
+                    "speedup_over_default": med.get("default", med["selected"]) / med["selected"],
+                    "reference_tiles_tflops": tf.get("reference_tiles", tf.get("default", tf["selected"])),
+                    "speedup_over_reference_tiles": med.get("reference_tiles", med.get("default", med["selected"]))
+                    / med["selected"],
                     "protocol": "6 alternating rounds of 10 warm-up + 50 timed launches each; medians",
                     "default_parity": default_parity}
+        if opts == dflt:
+            autotune["note"] = ("the cost model's pick is the autotuned configuration "
+                                "(tensorforge_amd/tuned_configs.json), so the speedup over it is 1")
         log(f"autotune: {autotune}")
 
     traffic = None
