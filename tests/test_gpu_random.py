@@ -12,6 +12,10 @@ the reference runner's method) bit for bit, and a masked mbr draw run unfused
 the fused kernel bit for bit (the fused epilogue performs the same IEEE
 operations in registers).
 
+16 more draws of the same kind come from the reference's own 105-configuration
+Stage 9 grid, whose 30 configurations without a whole-wave tile of their own
+run on a stand-in wave layout.
+
 A third GEMM family draws 24 cases from the promote=0 / vectorize=0
 instantiations (the ablation rungs, masked twins included) and from
 promote=1 vectorize=1 ones with xcd-swizzle=0, at random shapes up to 400 and
@@ -55,6 +59,26 @@ def _draws(count=48, seed=2026):
         slabs = -(-kk // cfg[4])
         split = int(rng.choice([1, 2, 3, 5, 8]))
         if split > slabs:
+            split = 1
+        out.append((wl, (m, n, k), cfg, split, masked))
+    return out
+
+
+def _reference_draws(count=16, seed=2031):
+    """Draws from the reference's own Stage 9 grid (python/costmodel.py:49-60),
+    stand-in wave layouts included, in the same form as _draws."""
+    rng = np.random.default_rng(seed)
+    space = cm.reference_space()
+    twins = {tuple(e["cfg"][:5]) for e in _lib.registry() if e["family"] == "staged" and e["name"].endswith("_masked")}
+    out = []
+    while len(out) < count:
+        wl = ("mbr", "matmul")[rng.integers(2)]
+        m, n, k = (int(v) for v in rng.integers(1, 701, size=3))
+        cfg = tuple(int(v) for v in space[rng.integers(len(space))])
+        masked = bool(rng.integers(2)) and (cfg[:2] + cm.kernel_tile(cfg) + cfg[4:5]) in twins
+        kk = k if masked else cm.padded(cfg, m, n, k)[2]
+        split = int(rng.choice([1, 2, 3]))
+        if split > -(-kk // cfg[4]):
             split = 1
         out.append((wl, (m, n, k), cfg, split, masked))
     return out
@@ -127,7 +151,7 @@ def _wave_draws(count=24, seed=2030):
     return out
 
 
-DRAWS = _draws()
+DRAWS = _draws() + _reference_draws()
 VARIANT_DRAWS = _variant_draws()
 WAVE_DRAWS = _wave_draws()
 ELT_DRAWS = _elt_draws()
