@@ -272,6 +272,59 @@ def record_best(path, workload, shape, best, pick, rho, objective="latency", sou
     path.write_text(json.dumps(table, indent=1, sort_keys=True) + "\n")
 
 
+def config_of(pipeline):
+    """(BM, BN, TM, TN, BK[, S[, 1]]) of a table row's pipeline text
+    (`tforge-gpu-pipeline{...}`, or the bare option string): the inverse of
+    costmodel.options."""
+    text = pipeline[pipeline.find("{") + 1:pipeline.rfind("}")] if "{" in pipeline else pipeline
+    kv = dict(tok.split("=", 1) for tok in text.split() if "=" in tok)
+    bm, bn = (int(v) for v in kv["block-tile"].split(","))
+    tm, tn = (int(v) for v in kv["thread-tile"].split(","))
+    cfg = (bm, bn, tm, tn, int(kv["tile-k"]))
+    s = int(kv.get("split-k", "1"))
+    if kv.get("wave-split-k") == "1":
+        return cfg + (s, 1)
+    return cfg + (s,) if s > 1 else cfg
+
+
+RESCORE_COLUMNS = ["commit", "date", "workload", "shape", "configs", "model_pick", "model_pick_ms", "best", "best_ms",
+                   "ratio_raw", "model_rank_of_best", "measured_rank_of_model_pick", "spearman_pred_vs_measured"]
+
+
+def rescore(csv_path, out_path=None):
+    """Scores the current cost model on measured studies, without a GPU: the
+    rows of `csv_path` grouped by study (workload, shape, commit, date), each
+    configuration predicted from its measured blocks per CU (the `params`
+    column), then the model's pick among the measured configurations against
+    the measured best and the Spearman correlation of predicted and measured
+    times, as a study's summary row computes them.  Returns the rows
+    (RESCORE_COLUMNS) and writes them to `out_path` if given."""
+    studies = {}
+    with open(csv_path, newline="") as fh:
+        for r in csv.DictReader(fh):
+            key = (r["commit"], r["date"], r["workload"], r["shape"])
+            bps = int(r["params"].split("blocks/SM=")[1].split()[0])
+            studies.setdefault(key, []).append((config_of(r["pipeline"]), bps, float(r["median_ms"])))
+    out = []
+    for (commit, date, workload, shape), rows in sorted(studies.items(), key=lambda kv: kv[0][1]):
+        m, n, k = (int(v) for v in shape.split("x"))
+        pred = [cm.predict(c, cm.padded(c, m, n, k), {"blocks_per_sm": b})["pred_ms"] for c, b, _ in rows]
+        meas = [ms for _, _, ms in rows]
+        by_pred = sorted(range(len(rows)), key=lambda i: pred[i])
+        by_meas = sorted(range(len(rows)), key=lambda i: meas[i])
+        pick, best = by_pred[0], by_meas[0]
+        rho = stats.spearmanr(pred, meas).statistic if len(rows) > 1 else float("nan")
+        out.append([commit, date, workload, shape, len(rows), cm.name(rows[pick][0]), f"{meas[pick]:.6f}",
+                    cm.name(rows[best][0]), f"{meas[best]:.6f}", f"{meas[best] / meas[pick]:.3f}",
+                    by_pred.index(best) + 1, by_meas.index(pick) + 1, f"{float(rho):.3f}"])
+    if out_path:
+        with open(out_path, "w", newline="") as fh:
+            w = csv.writer(fh)
+            w.writerow(RESCORE_COLUMNS)
+            w.writerows(out)
+    return out
+
+
 def default_summary(workload, space):
     """One summary file per workload and space, each with the reference's
     columns (bench/stage9_costmodel.py:58-61), so rows of different studies
@@ -300,6 +353,9 @@ def cli():
     ap.add_argument("--wave-split", action="store_true",
                     help="add the wave-split configurations (wave-split-k=1) to the space")
     ap.add_argument("--prewarm", type=int, default=500, help="untimed launches before the first timing of a shape")
+    ap.add_argument("--rescore", metavar="OUT", default=None,
+                    help="no GPU: score the current cost model on the studies already in --csv and write one row "
+                         "per study to OUT")
     ap.add_argument("--objective", choices=("latency", "throughput"), default="latency",
                     help="what the recorded configuration minimises: the per-launch median (tf_bench), or the "
                          "time per launch with launches back to back (bench.py's measure)")
@@ -308,6 +364,11 @@ def cli():
 
 def main(argv=None):
     args = cli().parse_args(argv)
+    if args.rescore:
+        for row in rescore(args.csv, args.rescore):
+            print(f"{row[2]:6s} {row[3]:16s} {row[0][:12]} n={row[4]:4d} pick {row[5]:22s} best {row[7]:22s} "
+                  f"ratio {row[9]} rank_best {row[10]:3d} spearman {row[12]}")
+        return 0
     table = provenance.ResultsTable(args.csv)
     base = table.base
     summary_path = pathlib.Path(args.summary or default_summary(args.workload, args.space))

@@ -29,16 +29,19 @@ replaces the per-step terms with what bounds the gfx950 MFMA kernel:
              per CU are bound by it.
   exposed    the loads of a slab are issued DEPTH slabs before its LDS write
              (two register staging sets where a thread stages at most 8
-             vectors per slab, else one set, 1.5 slabs ahead), so
-             max(0, LATENCY - DEPTH * compute) is exposed per slab.
+             vectors per slab, else one set), so max(0, LATENCY - DEPTH *
+             compute) is exposed per slab (DEPTH 2 or 1).
+  serial     with one wave per SIMD and the slab staged in one burst (not
+             spread over the MFMAs) nothing overlaps a wave's fragment reads
+             with its MFMAs: the step is at least mfma_step + lds_step.
   sync       one barrier per slab; measured to cost nothing visible in the
              launch time (the waves' MFMAs cover it), so 0.
   efficiency of the kernel structure (calibrated on the Stage 9 measurements):
              16x16 MFMA blocks (v_mfma_f32_16x16x4_f32: twice the
-             instructions and fragment reads per FLOP) and block-staged
-             kernels (the staging burst between two chunks of MFMAs, rather
-             than one staging operation after each MFMA) each run at 1/1.05
-             of the MFMA rate.
+             instructions and fragment reads per FLOP) run at 1/1.05 of the
+             MFMA rate, block-staged kernels (the staging burst between two
+             chunks of MFMAs, rather than one staging operation after each
+             MFMA) at 1/1.10.
 
 Split-K (a backend option, a sixth configuration entry S): S workgroups per
 output tile, each over Kp/S; the tile count is multiplied by S and the K
@@ -62,11 +65,13 @@ stream, the shortest reduction kernel); LATENCY, the structure divisor 1.05
 and the wave-split big-tile efficiency 0.55 (from the 64 x 4096 x 4096
 measurements, where the wave-split family is the one that matters) are
 calibrated on the Stage 9 measurements, and the model only ranks
-configurations.  Over the 22 (workload, shape) studies of the tuned shapes
-its pick reached 0.90-1.00 of the measured best (mean 0.987); the terms that
-moved it there from 0.82-1.00 are the L2 stream rate for small tiles, the
-staging depth in the exposed latency, the first-slab prologue and the
-structure divisor.
+configurations.  Over the 25 measured studies (results/gpu/stage9_autotune.csv,
+rescored by bench/stage9_costmodel.py --rescore) its pick reaches 0.90-1.00
+of the measured best (mean 0.986) and its Spearman rank correlation with the
+measured times 0.48-0.98 (mean 0.82); the terms that moved the pick there
+from 0.82-1.00 are the L2 stream rate for small tiles, the staging depth in
+the exposed latency, the first-slab prologue and the structure divisors, and
+the serial term lifted the mean correlation from 0.76.
 """
 
 import dataclasses
@@ -98,7 +103,8 @@ class Target:
     launch_s: float = 3e-6              # mfma: one more dependent kernel launch (split-K reduction)
     reduce_min_s: float = 2.5e-6        # mfma: shortest reduction kernel (measured 3.3-4.0 us at 64 x 4096)
     l2_stream_bytes_per_cycle: float = 22.0  # mfma: measured per-CU L2 -> CU stream (L2 requests in flight)
-    slow_structure: float = 1.05        # mfma: MFMA-rate divisor for 16x16 blocks and for block staging
+    slow_structure: float = 1.05        # mfma: MFMA-rate divisor for 16x16 blocks
+    slow_block_staging: float = 1.10    # mfma: MFMA-rate divisor for block staging (not spread over the MFMAs)
     wave_split_big_tile: float = 0.55   # mfma: MFMA efficiency of wave-split tiles of >= 4 32x32 blocks
 
 
@@ -331,14 +337,18 @@ def predict(cfg, padded, info, clock_mhz=None, target=MI355X):
     q = math.ceil(resident * w / target.simds)
     # FP32 MFMA: 64 FLOP per SIMD clock for both block sizes (4096 FLOP in 64
     # cycles, or 2048 in 32); a wave's slab is 2 * (8 TM)(8 TN) BK FLOP.
-    slow = (target.slow_structure if mb == 16 else 1.0) * (1.0 if spread else target.slow_structure)
+    slow = (target.slow_structure if mb == 16 else 1.0) * (1.0 if spread else target.slow_block_staging)
     mfma_step = q * 2 * (8 * tm) * (8 * tn) * bk / 64.0 * (target.mfma_cycles / 64.0) * slow
     # per chunk of 256 / mb k values, 1 KiB per A block-row and per B block-column
     lds_bytes = resident * (w * (bk / (256 // mb)) * 1024 * (fm + fn) + (bm + bn) * bk * 4)
     lds_step = lds_bytes / target.lds_bytes_per_cycle
     l2_step = resident * (bm + bn) * bk * 4 / target.l2_stream_bytes_per_cycle
     compute = max(mfma_step, lds_step, l2_step)
-    exposed = max(0.0, target.latency - (2.0 if depth == 2 else 1.5) * compute)
+    if q == 1 and not spread:
+        # one wave per SIMD and the slab staged in one burst: no other wave
+        # issues MFMAs while this one reads its fragments from LDS
+        compute = max(compute, mfma_step + lds_step)
+    exposed = max(0.0, target.latency - (2.0 if depth == 2 else 1.0) * compute)
     step = compute + exposed + target.sync / q
     epilogue = target.latency + resident * bm * bn * 4 / target.l2_bytes_per_cycle
     # the first slab of every resident workgroup arrives before any MFMA

@@ -1,6 +1,7 @@
 """The cost model: the reference formula restated exactly (pinned by the
 reference's own Stage 9 result rows), and the CDNA4 retarget's invariants."""
 
+import csv
 import json
 import pathlib
 
@@ -10,6 +11,7 @@ from tensorforge_amd import costmodel as cm
 
 GOLDEN = json.loads((pathlib.Path(__file__).resolve().parent / "golden" / "stage9_costmodel.json").read_text())
 ROWS = [dict(zip(GOLDEN["columns"], r)) for r in GOLDEN["rows"]]
+RESULTS = pathlib.Path(__file__).resolve().parents[1] / "results" / "gpu"
 
 
 def test_reference_formula_reproduces_stage9_rows():
@@ -98,3 +100,53 @@ def test_split_k_model_terms():
     assert cm.predict(c + (2,), big, inf)["pred_ms"] > cm.predict(c, big, inf)["pred_ms"]
     assert len(cm.default_config(2048, 2048, 2048)) == 5
     assert cm.splits_of(cm.default_config(64, 4096, 4096)) > 1
+
+
+def test_config_of_inverts_options():
+    from tensorforge_amd.bench import stage9_costmodel as s9
+    for cfg in cm.config_space()[::7] + cm.wave_split_space()[::5]:
+        for c in {tuple(cfg[:5]), tuple(cfg[:5]) + (4,)} if not cm.wave_split_of(cfg) else {cfg, cfg[:5] + (4, 1)}:
+            assert s9.config_of("tforge-gpu-pipeline{" + cm.options(c) + "}") == c
+            assert s9.config_of(cm.options(c) + " mask-edges=1") == c
+
+
+def _summaries():
+    rows = []
+    for name in ("stage9_summary.csv", "stage9_summary_matmul.csv", "stage9_summary_reference_space.csv"):
+        with open(RESULTS / name, newline="") as fh:
+            rows += [dict(r, workload="matmul" if "matmul" in name else "mbr") for r in csv.DictReader(fh)]
+    return rows
+
+
+def test_rescore_reproduces_the_recorded_studies():
+    """Rescoring the committed per-configuration rows finds, for every study
+    in the summaries, the same configurations, the same measured best and
+    its time: the rows and the summaries describe the same runs."""
+    from tensorforge_amd.bench import stage9_costmodel as s9
+    got = {(r[0], r[2], r[3], r[4]): r for r in s9.rescore(RESULTS / "stage9_autotune.csv")}
+    for s in _summaries():
+        r = got[(s["commit"], s["workload"], s["shape"], int(s["configs_compiled"]))]
+        assert (r[7], r[8]) == (s["best"], s["best_ms"]), s
+
+
+def test_rescore_file_is_the_current_model():
+    """results/gpu/stage9_rescore.csv is what the current model scores on the
+    committed rows, and the quality the cost model's docstring states holds:
+    every pick within 0.90 of the measured best, mean Spearman above 0.8."""
+    from tensorforge_amd.bench import stage9_costmodel as s9
+    rows = s9.rescore(RESULTS / "stage9_autotune.csv")
+    with open(RESULTS / "stage9_rescore.csv", newline="") as fh:
+        committed = list(csv.reader(fh))
+    assert committed[0] == s9.RESCORE_COLUMNS
+    assert committed[1:] == [[str(v) for v in r] for r in rows]
+    assert min(float(r[9]) for r in rows) >= 0.90
+    assert sum(float(r[12]) for r in rows) / len(rows) > 0.80
+
+
+def test_rescore_sees_a_planted_inversion(monkeypatch):
+    """A model whose prediction is inverted ranks the measurements backwards."""
+    from tensorforge_amd.bench import stage9_costmodel as s9
+    real = cm.predict
+    monkeypatch.setattr(cm, "predict", lambda *a, **k: {"pred_ms": 1.0 / real(*a, **k)["pred_ms"]})
+    rows = s9.rescore(RESULTS / "stage9_autotune.csv")
+    assert all(float(r[12]) < 0 for r in rows)
