@@ -6,8 +6,10 @@ MI355X, through libtforge_hip (the gfx950 staged MFMA kernel).
                   [--no-cpu-baseline] [--no-autotune-compare]
   python bench.py --cpu-table results/cpu/cpu_baseline_host.csv   (CPU rows only)
 
-A step is one launch of the compiled program over device-resident inputs
-(A, B, bias uniform[-1,1] from seed 1234, row-major).  Order of work:
+A step is one launch of the compiled program over device-resident inputs:
+the reference's seeded draws (numpy default_rng(1234), uniform[-1,1] in the
+order A, B, bias; python/tforge_cpu.py:89-100), made on the host and uploaded
+before any timing.  Order of work:
 
   1. pre-warm (disclosed in the line): launches in chunks of 20 until at least
      0.3 s have passed and the last three chunks' per-launch times agree within
@@ -133,9 +135,14 @@ class Launcher:
                         "last_chunk_us": round(chunks[-1] * 1e3, 2)}
 
 
-def parity_sample(torch, A, B, bias, C, rows=64):
+# err/bound of the reference's own kernels on the same inputs (ref:results/gpu/stage8.csv:86).
+REFERENCE_ERR_OVER_BOUND = 0.00232
+
+
+def parity_sample(torch, A, B, bias, C, rows=M):
     """err/bound of the reference check (python/tforge_gpu.py:134-145) with
-    the ReLU mask rule, on a sample of output rows, in float64 on the GPU."""
+    the ReLU mask rule, in float64 on the GPU, over `rows` evenly spaced output
+    rows (all of them by default)."""
     idx = torch.linspace(0, M - 1, rows, device=A.device).long()
     a64, b64, c64 = A[idx].double(), B.double(), bias.double()
     z = a64 @ b64 + c64
@@ -149,6 +156,7 @@ def parity_sample(torch, A, B, bias, C, rows=64):
     decided = z.abs() > bound
     masks = int((decided & ((out == 0) != (z <= 0))).sum())
     return {"rows_checked": rows, "err_over_bound": eob, "mask_mismatches": masks,
+            "reference_kernels_err_over_bound": REFERENCE_ERR_OVER_BOUND,
             "pass": eob <= 1.0 and masks == 0 and not bool(torch.isnan(out).any())}
 
 
@@ -313,11 +321,8 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(1234)
-    A = torch.empty((M, K), device=dev, dtype=torch.float32).uniform_(-1, 1, generator=gen)
-    B = torch.empty((K, N), device=dev, dtype=torch.float32).uniform_(-1, 1, generator=gen)
-    bias = torch.empty((N,), device=dev, dtype=torch.float32).uniform_(-1, 1, generator=gen)
+    host = tc.make_inputs("mbr", M, N, K, seed=1234)
+    A, B, bias = (torch.from_numpy(host[s]).to(dev) for s in ("a", "b", "bias"))
     C = torch.empty((M, N), device=dev, dtype=torch.float32)
     ptrs = [A.data_ptr(), B.data_ptr(), bias.data_ptr(), C.data_ptr()]
     stream = torch.cuda.current_stream()
@@ -391,7 +396,8 @@ def main():
     line = {
         "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": window_ms, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32", "data": "synthetic: A, B, bias uniform[-1,1] (torch, seed 1234)",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic: A, B, bias uniform[-1,1], the reference's draws "
+                                                   "(numpy default_rng(1234), python/tforge_cpu.py:89-100)",
         "config": {"workload": f"fused mbr relu(A@B+bias) fp32 M=N=K={M}, row-major", "options": opts,
                    "kernel": launch["kernel"], "grid": launch["grid"], "block": launch["block"],
                    "parallelism": "single GPU"},
