@@ -65,9 +65,9 @@ stream, the shortest reduction kernel); LATENCY, the structure divisor 1.05
 and the wave-split big-tile efficiency 0.55 (from the 64 x 4096 x 4096
 measurements, where the wave-split family is the one that matters) are
 calibrated on the Stage 9 measurements, and the model only ranks
-configurations.  Over the 25 measured studies (results/gpu/stage9_autotune.csv,
+configurations.  Over the 27 measured studies (results/gpu/stage9_autotune.csv,
 rescored by bench/stage9_costmodel.py --rescore) its pick reaches 0.90-1.00
-of the measured best (mean 0.986) and its Spearman rank correlation with the
+of the measured best (mean 0.983) and its Spearman rank correlation with the
 measured times 0.48-0.98 (mean 0.82); the terms that moved the pick there
 from 0.82-1.00 are the L2 stream rate for small tiles, the staging depth in
 the exposed latency, the first-slab prologue and the structure divisors, and
