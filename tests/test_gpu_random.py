@@ -1,6 +1,6 @@
 """A seeded random sweep over the staged path's option space, through tf_run.
 
-48 draws (seed 2026): workload mbr or matmul; each of M, N, K uniform in
+144 draws (seed 2026): workload mbr or matmul; each of M, N, K uniform in
 1..700; a configuration from the 224-entry CDNA4 space; a split-K factor from
 1, 2, 3, 5, 8 (at most the problem's K slabs); mask-edges on or off (on only
 for configurations that have a masked twin).  Every draw meets the reference's
@@ -12,22 +12,22 @@ the reference runner's method) bit for bit, and a masked mbr draw run unfused
 the fused kernel bit for bit (the fused epilogue performs the same IEEE
 operations in registers).
 
-16 more draws of the same kind come from the reference's own 105-configuration
+48 more draws of the same kind come from the reference's own 105-configuration
 Stage 9 grid, whose 30 configurations without a whole-wave tile of their own
 run on a stand-in wave layout.
 
-A third GEMM family draws 24 cases from the promote=0 / vectorize=0
+A third GEMM family draws 64 cases from the promote=0 / vectorize=0
 instantiations (the ablation rungs, masked twins included) and from
 promote=1 vectorize=1 ones with xcd-swizzle=0, at random shapes up to 400 and
 split factors up to 3.
 
-A fourth draws 24 wave-split configurations (wave-split-k=1; every entry of
+A fourth draws 72 wave-split configurations (wave-split-k=1; every entry of
 the cost model's wave-split space is eligible) at random shapes up to 700,
 compiled at the padded shape, with split factors 1, 2 or 3.
 
-Two more families: 32 element-op programs (relu, bias_add, add; shapes up to
+Two more families: 64 element-op programs (relu, bias_add, add; shapes up to
 3000 x 8192, half of them with rows of whole workgroup chunks; every thread tile 1..8 x 1..8 that compiles) bit-exact against
-NumPy float32 (python/tforge_gpu.py:116-126), and 16 residual blocks at ragged
+NumPy float32 (python/tforge_gpu.py:116-126), and 32 residual blocks at ragged
 shapes with masked tiles against the two-layer composed bound.
 """
 
@@ -45,7 +45,7 @@ pytestmark = pytest.mark.gpu
 STAGED = "block-tile={},{} thread-tile={},{} tile-k={} promote=1 vectorize=1"
 
 
-def _draws(count=48, seed=2026):
+def _draws(count=144, seed=2026):
     rng = np.random.default_rng(seed)
     space = list(cm.config_space())
     twins = {tuple(e["cfg"][:5]) for e in _lib.registry() if e["family"] == "staged" and e["name"].endswith("_masked")}
@@ -64,7 +64,7 @@ def _draws(count=48, seed=2026):
     return out
 
 
-def _reference_draws(count=16, seed=2031):
+def _reference_draws(count=48, seed=2031):
     """Draws from the reference's own Stage 9 grid (python/costmodel.py:49-60),
     stand-in wave layouts included, in the same form as _draws."""
     rng = np.random.default_rng(seed)
@@ -84,7 +84,7 @@ def _reference_draws(count=16, seed=2031):
     return out
 
 
-def _elt_draws(count=32, seed=2027):
+def _elt_draws(count=64, seed=2027):
     rng = np.random.default_rng(seed)
     out = []
     while len(out) < count:
@@ -103,7 +103,7 @@ def _elt_draws(count=32, seed=2027):
     return out
 
 
-def _resmlp_draws(count=16, seed=2028):
+def _resmlp_draws(count=32, seed=2028):
     rng = np.random.default_rng(seed)
     space = [tuple(e["cfg"][:5]) for e in _lib.registry() if e["family"] == "staged" and e["name"].endswith("_masked")
              and e["cfg"][5] == 1 and e["cfg"][6] == 1]
@@ -114,7 +114,7 @@ def _resmlp_draws(count=16, seed=2028):
     return out
 
 
-def _variant_draws(count=24, seed=2029):
+def _variant_draws(count=64, seed=2029):
     """The promote=0 / vectorize=0 instantiations (the ablation rungs) and
     promote=1 vectorize=1 ones with the XCD tile order switched off."""
     rng = np.random.default_rng(seed)
@@ -138,7 +138,7 @@ def _variant_draws(count=24, seed=2029):
     return out
 
 
-def _wave_draws(count=24, seed=2030):
+def _wave_draws(count=72, seed=2030):
     rng = np.random.default_rng(seed)
     space = cm.wave_split_space()
     out = []
