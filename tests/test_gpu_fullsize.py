@@ -89,12 +89,17 @@ def test_full_size_properties(workload, m, n, k):
         assert o.mask_mismatches(got, o.preactivation64(ins), bound) == 0
 
 
-def test_full_size_residual_block():
+# The residual block's measured best tiles (results/gpu/resmlp.csv) and the earlier pick.
+RESMLP_OPTS = ["block-tile=128,128 thread-tile=8,8 tile-k=16 promote=1 vectorize=1",
+               "block-tile=128,256 thread-tile=8,4 tile-k=32 promote=1 vectorize=1"]
+
+
+@pytest.mark.parametrize("opts", RESMLP_OPTS)
+def test_full_size_residual_block(opts):
     """The residual block at its benchmark size (x 4096x2048, W1 2048x8192,
-    W2 8192x2048) with the measured best tiles."""
+    W2 8192x2048)."""
     torch, dev = _torch()
     m, n, k = 4096, 2048, 8192
-    opts = "block-tile=128,256 thread-tile=8,4 tile-k=32 promote=1 vectorize=1"
     kern = _lib.Kernel(tc.gen_mlir("resmlp", m, n, k), opts, "t.mlir")
     stream = torch.cuda.current_stream().cuda_stream
     host = tc.make_inputs("resmlp", m, n, k)
@@ -142,7 +147,7 @@ def test_full_size_residual_layers_against_the_oracle():
     the two checks cover it."""
     torch, dev = _torch()
     m, n, k = 4096, 2048, 8192
-    opts = "block-tile=128,256 thread-tile=8,4 tile-k=32 promote=1 vectorize=1"
+    opts = RESMLP_OPTS[0]
     stream = torch.cuda.current_stream().cuda_stream
     host = tc.make_inputs("resmlp", m, n, k)
     x, w1, b1, w2, b2 = (torch.from_numpy(np.ascontiguousarray(host[s])).to(dev) for s in ("x", "w1", "b1", "w2", "b2"))
