@@ -117,6 +117,12 @@ class Kernel:
         self.h = P()
         check(L.tf_compile(source_name.encode(), program.encode(), options.encode(), ctypes.byref(self.h)))
         self.program, self.options = program, options
+        # The buffer list is fixed at compile time; launch() validates against
+        # this copy instead of asking the library on every call (a launch of a
+        # small problem is otherwise bound by those calls, not by the GPU).
+        self._bufs = self.buffers()
+        self._sizes = [b["shape"][0] * b["shape"][1] for b in self._bufs]
+        self._launch_fn = L.tf_launch
 
     def __del__(self):
         h = getattr(self, "h", None)
@@ -166,7 +172,7 @@ class Kernel:
     def _check_host(self, arrays, out, logical):
         # tf_run copies whole buffers from and to these pointers: a short,
         # strided or non-float32 array would be read or written out of bounds.
-        nargs = len(self.buffers()) - 1
+        nargs = len(self._bufs) - 1
         if len(arrays) != nargs:
             raise ValueError(f"this program takes {nargs} input arrays, got {len(arrays)}")
         want = [r * c for r, c in self.host_shapes(logical)]
@@ -180,21 +186,24 @@ class Kernel:
                 raise ValueError(f"{what} has {a.size} elements, the program needs {size}")
 
     def launch(self, device_ptrs, stream=0):
-        bufs = self.buffers()
-        if len(device_ptrs) != len(bufs):
-            raise ValueError(f"this program takes {len(bufs)} device buffers (inputs, then the output), "
+        n = len(self._sizes)
+        if len(device_ptrs) != n:
+            raise ValueError(f"this program takes {n} device buffers (inputs, then the output), "
                              f"got {len(device_ptrs)}")
-        for i, (p, b) in enumerate(zip(device_ptrs, bufs)):
-            if not int(p) and b["shape"][0] * b["shape"][1] > 0:
-                raise ValueError(f"device buffer {i} ({b['name']}) is a null pointer")
-        arr = (P * len(device_ptrs))(*[P(int(p)) for p in device_ptrs])
-        check(lib().tf_launch(self.h, arr, P(int(stream)) if stream else None))
+        ptrs = [int(p) for p in device_ptrs]
+        if not all(ptrs):
+            for i, p in enumerate(ptrs):
+                if not p and self._sizes[i] > 0:
+                    raise ValueError(f"device buffer {i} ({self._bufs[i]['name']}) is a null pointer")
+        rc = self._launch_fn(self.h, (P * n)(*ptrs), int(stream) or None)
+        if rc < 0:
+            check(rc)
 
     def launch_noalloc(self, device_ptrs, stream=0):
         """tf_launch_noalloc: the same launches with the library's fixed
         per-GPU scratch array; calls that overlap on one GPU race."""
-        if len(device_ptrs) != len(self.buffers()):
-            raise ValueError(f"this program takes {len(self.buffers())} device buffers, got {len(device_ptrs)}")
+        if len(device_ptrs) != len(self._sizes):
+            raise ValueError(f"this program takes {len(self._sizes)} device buffers, got {len(device_ptrs)}")
         arr = (P * len(device_ptrs))(*[P(int(p)) for p in device_ptrs])
         check(lib().tf_launch_noalloc(self.h, arr, P(int(stream)) if stream else None))
 
